@@ -1,0 +1,71 @@
+"""Build recipe for the gfx950 GEMM library.
+
+    python 5_amd/csrc/build.py [-v]
+
+compiles 5_amd/csrc/hcg_gemm.hip (kernels + the C ABI declared in
+include/hcg_gemm.h) with hipcc for gfx950 into
+5_amd/hc/gfx950/libhcg_gfx950.so, next to the Python code that loads it.
+hipcc cross-compiles, so this runs on a machine without a GPU.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+ROOT = os.path.dirname(PKG)
+SRC = os.path.join(HERE, "hcg_gemm.hip")
+INCLUDE = os.path.join(ROOT, "include")
+OUT = os.path.join(PKG, "hc", "gfx950", "libhcg_gfx950.so")
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def flags() -> list[str]:
+    return [
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        # Packed fp32 VALU forms stay disabled for all device code.
+        "-Xclang",
+        "-target-feature",
+        "-Xclang",
+        "-packed-fp32-ops",
+        f"-I{INCLUDE}",
+        "-Wall",
+    ]
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(os.path.dirname(OUT), exist_ok=True)
+    tmp = OUT + ".tmp"
+    cmd = [hipcc(), *flags(), SRC, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # The host pass does not know the device-only target feature; that
+    # warning is expected and harmless.  Anything else is shown.
+    noise = "'-packed-fp32-ops' is not a recognized feature for this target"
+    err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
+    if verbose and err.strip():
+        print(err)
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

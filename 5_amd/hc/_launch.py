@@ -1,0 +1,235 @@
+"""Launch binding and geometry validation shared by every hc target.
+
+Follows the reference's pre-execution phase (hc/simulator.py:189-229):
+kernel metadata lookup (:657-661), binding the launch arguments without the
+group parameter (:664-672), binding Buffer extents to symbols with conflict
+detection (:675-683, :752-791), resolving ``work_shape``/``group_shape``/
+``subgroup_size`` (:797-855) and validating the geometry (:858-900).  Symbol
+errors surface as ``LaunchError`` (:227-228).
+
+Buffers may be ``numpy.ndarray`` (as in the reference) or ``torch.Tensor``
+(device buffers that a gfx950 launch uses in place).
+"""
+
+from __future__ import annotations
+
+import inspect
+from dataclasses import dataclass
+from typing import Any, get_args, get_origin
+
+from ._errors import LaunchError
+from .core import BufferSpec, KernelMetadata
+from .symbols import Bindings, Env, Expr, Symbol, SymbolError, sym
+
+
+@dataclass(frozen=True)
+class PreparedLaunch:
+    fn: Any
+    bound: inspect.BoundArguments
+    env: Env
+    literal_names: frozenset[str]
+    work_shape: tuple[int, ...]
+    group_shape: tuple[int, ...]
+    subgroup_size: int | None
+    buffer_params: tuple[str, ...]
+
+    @property
+    def is_empty(self) -> bool:
+        return any(dim == 0 for dim in self.work_shape)
+
+
+def buffer_dtype_name(value: Any) -> str | None:
+    """dtype name of a numpy array or torch tensor, else None."""
+    import numpy as np
+
+    if isinstance(value, np.ndarray):
+        return str(value.dtype.name)
+    torch = _torch_if_loaded()
+    if torch is not None and isinstance(value, torch.Tensor):
+        return str(value.dtype).replace("torch.", "")
+    return None
+
+
+def _torch_if_loaded() -> Any:
+    import sys
+
+    return sys.modules.get("torch")
+
+
+def is_buffer(value: Any) -> bool:
+    return buffer_dtype_name(value) is not None
+
+
+def kernel_metadata(fn: Any) -> KernelMetadata:
+    metadata = getattr(fn, "__hc_kernel__", None)
+    if metadata is None:
+        raise LaunchError("launch() expects a function decorated with @kernel")
+    return metadata
+
+
+def _bind_arguments(fn: Any, args: tuple[Any, ...], kwargs: dict[str, Any]) -> inspect.BoundArguments:
+    params = list(inspect.signature(fn).parameters.values())
+    if not params:
+        raise LaunchError("kernel must accept a CurrentGroup parameter")
+    try:
+        return inspect.Signature(params[1:]).bind(*args, **kwargs)
+    except TypeError as exc:
+        raise LaunchError(f"cannot bind launch arguments: {exc}") from exc
+
+
+class _AnnotationLocals(dict):
+    """Unknown capitalised names in string annotations resolve to symbols."""
+
+    def __missing__(self, name: str) -> Any:
+        if name[:1].isupper():
+            return getattr(sym, name)
+        raise KeyError(name)
+
+
+def resolved_annotations(fn: Any) -> dict[str, Any]:
+    raw = inspect.get_annotations(fn, eval_str=False)
+    if not any(isinstance(a, str) for a in raw.values()):
+        return dict(raw)
+    localns = _AnnotationLocals(fn.__globals__)
+    closure = inspect.getclosurevars(fn)
+    localns.update(closure.nonlocals)
+    resolved: dict[str, Any] = {}
+    for name, annotation in raw.items():
+        if not isinstance(annotation, str):
+            resolved[name] = annotation
+            continue
+        try:
+            resolved[name] = eval(annotation, fn.__globals__, localns)  # noqa: S307 - annotation text
+        except (NameError, TypeError) as exc:
+            raise LaunchError(f"failed to resolve annotations for {fn.__name__}") from exc
+    return resolved
+
+
+def _bind_dimension(bindings: Bindings, dim: Any, value: int, source: str) -> None:
+    if isinstance(dim, Symbol):
+        bindings.bind(dim, value, source=source)
+    elif isinstance(dim, Expr):
+        bindings.require(dim, value, source=source)
+    elif isinstance(dim, int) and not isinstance(dim, bool) and dim != value:
+        raise LaunchError(f"{source} expected {dim}, got {value}")
+
+
+def _bind_buffer(bindings: Bindings, spec: BufferSpec, value: Any, source: str) -> None:
+    dtype = buffer_dtype_name(value)
+    if dtype is None:
+        raise LaunchError(f"{source} must be a numpy.ndarray or torch.Tensor buffer")
+    shape = tuple(int(d) for d in value.shape)
+    if len(shape) != len(spec.dimensions):
+        raise LaunchError(f"{source} rank does not match its Buffer annotation")
+    if spec.dtype is not None and dtype != spec.dtype:
+        raise LaunchError(f"{source} dtype expected {spec.dtype}, got {dtype}")
+    for index, dim in enumerate(spec.dimensions):
+        _bind_dimension(bindings, dim, shape[index], f"{source}.shape[{index}]")
+
+
+def _bind_tuple(bindings: Bindings, dims: tuple[Any, ...], value: Any, source: str) -> None:
+    if not isinstance(value, tuple):
+        raise LaunchError(f"{source} must be a tuple")
+    if len(value) != len(dims):
+        raise LaunchError(f"{source} length does not match its tuple annotation")
+    for index, (dim, item) in enumerate(zip(dims, value)):
+        _bind_dimension(bindings, dim, int(item), f"{source}[{index}]")
+
+
+def _resolve_dim(value: Any, env: Env, literal_names: frozenset[str], *, static: bool, name: str) -> int:
+    import numpy as np
+
+    if isinstance(value, bool):
+        raise LaunchError(f"{name} must be an integer")
+    if isinstance(value, (int, np.integer)):
+        return int(value)
+    if isinstance(value, Expr):
+        if static and not {s.name for s in value.free_symbols()} <= literal_names:
+            raise LaunchError(f"{name} must be constant or use only literal symbols")
+        return int(value.eval(env))
+    raise LaunchError(f"{name} must be an integer expression")
+
+
+def _resolve_shape(spec: Any, env: Env, literal_names: frozenset[str]) -> tuple[int, ...]:
+    if spec is None:
+        raise LaunchError("kernel metadata is missing required work_shape")
+    values = spec if isinstance(spec, tuple) else (spec,)
+    return tuple(_resolve_dim(v, env, literal_names, static=False, name="shape") for v in values)
+
+
+def _validate(work: tuple[int, ...], group: tuple[int, ...], subgroup: int | None, limit: int | None) -> None:
+    if len(work) != len(group):
+        raise LaunchError("work_shape and group_shape must have the same rank")
+    if any(d < 0 for d in work):
+        raise LaunchError("work_shape values must be non-negative")
+    if any(d <= 0 for d in group):
+        raise LaunchError("group_shape values must be positive")
+    if subgroup is not None:
+        if subgroup <= 0:
+            raise LaunchError("subgroup_size must be positive")
+        if group and group[0] % subgroup != 0:
+            raise LaunchError("group_shape[0] must be divisible by subgroup_size")
+    if limit is not None:
+        size = 1
+        for d in group:
+            size *= d
+        if size > limit:
+            raise LaunchError("group size exceeds the target limit")
+
+
+def _align_up(value: int, align: int) -> int:
+    return -(-value // align) * align
+
+
+def default_group_shape(work_shape: tuple[int, ...], subgroup_size: int | None) -> tuple[int, ...]:
+    """Default group shape when a kernel gives none (hc/simulator.py:67-73)."""
+    base = tuple(max(1, d) for d in work_shape)
+    if not base or subgroup_size is None:
+        return base
+    return (_align_up(base[0], subgroup_size), *base[1:])
+
+
+def prepare_launch(fn: Any, args: tuple[Any, ...], kwargs: dict[str, Any], target: Any) -> PreparedLaunch:
+    try:
+        metadata = kernel_metadata(fn)
+        bound = _bind_arguments(fn, args, kwargs)
+        annotations = resolved_annotations(fn)
+        bindings = Bindings()
+        buffer_params: list[str] = []
+        for name, value in bound.arguments.items():
+            annotation = annotations.get(name, inspect.Signature.empty)
+            if isinstance(annotation, BufferSpec):
+                _bind_buffer(bindings, annotation, value, name)
+                buffer_params.append(name)
+            elif get_origin(annotation) is tuple:
+                _bind_tuple(bindings, get_args(annotation), value, name)
+        env = bindings.freeze()
+        literal_names = frozenset(s.name for s in metadata.literals if isinstance(s, Symbol))
+        work_shape = _resolve_shape(metadata.work_shape, env, literal_names)
+        subgroup_size = (
+            None
+            if metadata.subgroup_size is None
+            else _resolve_dim(metadata.subgroup_size, env, literal_names, static=True, name="subgroup_size")
+        )
+        if metadata.group_shape is None:
+            chooser = getattr(target, "choose_group_shape", None)
+            group_shape = (
+                chooser(work_shape, subgroup_size)
+                if chooser is not None
+                else default_group_shape(work_shape, subgroup_size)
+            )
+        else:
+            group_shape = _resolve_shape(metadata.group_shape, env, literal_names)
+        _validate(work_shape, group_shape, subgroup_size, getattr(target, "max_group_size", None))
+    except SymbolError as exc:
+        raise LaunchError(str(exc)) from exc
+    return PreparedLaunch(
+        fn=fn,
+        bound=bound,
+        env=env,
+        literal_names=literal_names,
+        work_shape=work_shape,
+        group_shape=group_shape,
+        subgroup_size=subgroup_size,
+        buffer_params=tuple(buffer_params),
+    )

@@ -1,0 +1,284 @@
+"""gfx950 (MI355X) launch target for hc kernels.
+
+``launch(fn, *args, target=Gfx950Target())`` keeps the reference launch
+contract (hc/simulator.py:165-186): the same argument binding and geometry
+validation (see ``hc._launch``), ``LaunchError`` before any execution, and a
+zero-size launch is a no-op.  It then runs the kernel as a whole on the GPU
+through the C ABI of libhcg_gfx950.so (include/hcg_gemm.h) instead of
+interpreting it workgroup by workgroup.
+
+Kernels are lowered as a whole, not intrinsic by intrinsic: the wave64 MFMA
+design replaces the reference's per-lane wave32 WMMA fragment contract
+(examples/amdgpu_gfx11_wmma_matmul.py:18-31), so no per-intrinsic mapping
+exists.  A kernel is accepted when
+
+* it was registered with :func:`register_kernel`, or
+* its name is one of :data:`KNOWN_GEMM_KERNELS` (the reference's
+  ``tiled_gfx11_wmma_matmul``, examples/amdgpu_gfx11_wmma_matmul.py:301-326,
+  and this package's ``tiled_gfx950_mfma_matmul``) and its buffer
+  signature is the contraction ``(Buffer[M, K, T], Buffer[K, N, T],
+  Buffer[M, N, float32])`` with T float16 or bfloat16.
+
+Anything else raises ``LaunchError`` naming the kernel.
+"""
+
+from __future__ import annotations
+
+import os
+from collections.abc import Callable
+from dataclasses import dataclass
+from typing import Any
+
+import numpy as np
+
+from .._errors import BackendError, LaunchError
+from .._launch import PreparedLaunch, buffer_dtype_name, prepare_launch, resolved_annotations
+from ..core import BufferSpec
+from ..symbols import Symbol
+from . import _native
+
+TARGET_NAME = "amdgpu-gfx950"
+
+KNOWN_GEMM_KERNELS = frozenset({"tiled_gfx11_wmma_matmul", "tiled_gfx950_mfma_matmul"})
+
+_DTYPE_CODES = {"float16": _native.HCG_F16, "bfloat16": _native.HCG_BF16}
+
+
+@dataclass(frozen=True)
+class Gfx950Target:
+    """Launch policy for gfx950 (the counterpart of ``SimulatorTarget``,
+    hc/simulator.py:60-75).
+
+    device: GPU index for host (numpy) buffers; device tensors run where they
+        live.  None = the current device.
+    algo: "auto" (by shape), "tiled" or "skinny" (M <= 16).
+    max_group_size: HIP's workgroup limit, checked like the simulator's.
+    """
+
+    device: int | None = None
+    algo: str = "auto"
+    max_group_size: int | None = 1024
+    name: str = TARGET_NAME
+
+    def choose_group_shape(self, work_shape: tuple[int, ...], subgroup_size: int | None) -> tuple[int, ...]:
+        base = tuple(max(1, d) for d in work_shape)
+        if not base or subgroup_size is None:
+            return base
+        return (-(-base[0] // subgroup_size) * subgroup_size, *base[1:])
+
+
+# --------------------------------------------------------------------------
+# Kernel lowering registry
+# --------------------------------------------------------------------------
+
+Lowering = Callable[[PreparedLaunch, Gfx950Target], None]
+
+_LOWERINGS: dict[Any, Lowering] = {}
+
+
+def _gemm_signature(fn: Any) -> tuple[str, str, str] | None:
+    """Names of the (A, B, C) parameters if ``fn`` has the contraction
+    signature, else None."""
+    annotations = resolved_annotations(fn)
+    specs = [(name, spec) for name, spec in annotations.items() if isinstance(spec, BufferSpec)]
+    if len(specs) != 3:
+        return None
+    (na, a), (nb, b), (nc, c) = specs
+    if not all(len(s.dimensions) == 2 for s in (a, b, c)):
+        return None
+    if not all(isinstance(d, Symbol) for s in (a, b, c) for d in s.dimensions):
+        return None
+    m, k = a.dimensions
+    k2, n = b.dimensions
+    m2, n2 = c.dimensions
+    if not (k == k2 and m == m2 and n == n2) or len({m, n, k}) != 3:
+        return None
+    if a.dtype != b.dtype or a.dtype not in _DTYPE_CODES or c.dtype != "float32":
+        return None
+    return na, nb, nc
+
+
+def _gemm_lowering(prepared: PreparedLaunch, target: Gfx950Target) -> None:
+    names = _gemm_signature(prepared.fn)
+    if names is None:
+        raise LaunchError(f"{prepared.fn.__name__} does not have a GEMM buffer signature")
+    args = prepared.bound.arguments
+    gemm(args[names[0]], args[names[1]], out=args[names[2]], algo=target.algo, device=target.device)
+
+
+def register_kernel(fn: Any, lowering: Lowering | str = "gemm") -> Any:
+    """Register a gfx950 lowering for kernel ``fn``.  ``"gemm"`` selects the
+    built-in GEMM lowering (the kernel must have the contraction signature)."""
+    if not hasattr(fn, "__hc_kernel__"):
+        raise LaunchError("register_kernel() expects a function decorated with @kernel")
+    if lowering == "gemm":
+        if _gemm_signature(fn) is None:
+            raise LaunchError(f"{fn.__name__} does not have a GEMM buffer signature")
+        lowering = _gemm_lowering
+    if not callable(lowering):
+        raise TypeError("lowering must be 'gemm' or a callable")
+    _LOWERINGS[fn] = lowering
+    return fn
+
+
+def find_lowering(fn: Any) -> Lowering:
+    lowering = _LOWERINGS.get(fn)
+    if lowering is not None:
+        return lowering
+    if getattr(fn, "__name__", None) in KNOWN_GEMM_KERNELS and _gemm_signature(fn) is not None:
+        return _gemm_lowering
+    raise LaunchError(f"no {TARGET_NAME} lowering for kernel {getattr(fn, '__name__', fn)!r}")
+
+
+def launch(fn: Any, *args: Any, target: Gfx950Target | None = None, **kwargs: Any) -> None:
+    """Launch an hc kernel on gfx950 (contract of hc/simulator.py:165-186)."""
+    runtime_target = Gfx950Target() if target is None else target
+    prepared = prepare_launch(fn, args, kwargs, runtime_target)
+    lowering = find_lowering(fn)
+    if prepared.is_empty:
+        return
+    lowering(prepared, runtime_target)
+
+
+run = launch
+
+
+# --------------------------------------------------------------------------
+# GEMM entry for numpy arrays and torch tensors
+# --------------------------------------------------------------------------
+
+
+def _torch():
+    try:
+        import torch
+    except ImportError as exc:  # pragma: no cover - torch is present on the targets
+        raise BackendError("the gfx950 backend needs PyTorch-ROCm for device memory") from exc
+    return torch
+
+
+def _row_stride(t: Any) -> int:
+    rows, cols = int(t.shape[0]), int(t.shape[1])
+    return int(t.stride(0)) if rows > 1 else max(cols, 1)
+
+
+def _check_shapes(a: Any, b: Any, c: Any | None) -> tuple[int, int, int]:
+    if len(a.shape) != 2 or len(b.shape) != 2:
+        raise LaunchError("A and B must be rank-2 matrices")
+    m, k = int(a.shape[0]), int(a.shape[1])
+    k2, n = int(b.shape[0]), int(b.shape[1])
+    if k != k2:
+        raise LaunchError("A.shape[1] must match B.shape[0]")
+    if c is not None and tuple(int(d) for d in c.shape) != (m, n):
+        raise LaunchError(f"C shape {tuple(c.shape)} does not match ({m}, {n})")
+    return m, n, k
+
+
+def _dtype_code(a: Any, b: Any) -> int:
+    da, db = buffer_dtype_name(a), buffer_dtype_name(b)
+    if da != db or da not in _DTYPE_CODES:
+        raise LaunchError(f"A and B must both be float16 or both bfloat16, got {da} and {db}")
+    return _DTYPE_CODES[da]
+
+
+def gemm(a: Any, b: Any, out: Any | None = None, *, algo: str = "auto", device: int | None = None) -> Any:
+    """C = A @ B on gfx950 with float32 accumulation and output.
+
+    Device tensors (torch, on a GPU) run in place on the current stream of
+    their device, asynchronously.  numpy arrays are copied to the device,
+    computed, and copied back into ``out`` (created if None); the call then
+    returns after the result is on the host.
+    """
+    if algo not in _native.ALGOS:
+        raise LaunchError(f"unknown algo {algo!r}; expected one of {sorted(_native.ALGOS)}")
+    algo_code = _native.ALGOS[algo]
+    torch_mod = _torch()
+    is_np = [isinstance(x, np.ndarray) for x in (a, b)]
+    if all(is_np) and (out is None or isinstance(out, np.ndarray)):
+        return _gemm_numpy(torch_mod, a, b, out, algo_code, device)
+    if not all(isinstance(x, torch_mod.Tensor) for x in (a, b)) or (
+        out is not None and not isinstance(out, torch_mod.Tensor)
+    ):
+        raise LaunchError("A, B and C must all be numpy arrays or all be torch tensors")
+    return _gemm_torch(torch_mod, a, b, out, algo_code)
+
+
+def _gemm_numpy(torch: Any, a: np.ndarray, b: np.ndarray, out: np.ndarray | None, algo: int, device: int | None) -> np.ndarray:
+    m, n, k = _check_shapes(a, b, out)
+    if out is not None and out.dtype != np.float32:
+        raise LaunchError(f"C dtype expected float32, got {out.dtype.name}")
+    dtype = _dtype_code(a, b)
+    if out is None:
+        out = np.empty((m, n), dtype=np.float32)
+    if m == 0 or n == 0:
+        return out
+    dev = torch.device("cuda", torch.cuda.current_device() if device is None else device)
+    with torch.cuda.device(dev):
+        ta = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+        tb = torch.from_numpy(np.ascontiguousarray(b)).to(dev)
+        tc = torch.empty((m, n), dtype=torch.float32, device=dev)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _native.gemm(algo, dtype, ta.data_ptr(), max(k, 1), tb.data_ptr(), n, tc.data_ptr(), n, m, n, k, stream)
+        out[...] = tc.cpu().numpy()
+    return out
+
+
+def _gemm_torch(torch: Any, a: Any, b: Any, out: Any | None, algo: int) -> Any:
+    m, n, k = _check_shapes(a, b, out)
+    if not (a.is_cuda and b.is_cuda) or (out is not None and not out.is_cuda):
+        raise LaunchError("torch tensors must live on a GPU")
+    if b.device != a.device or (out is not None and out.device != a.device):
+        raise LaunchError("A, B and C must live on the same device")
+    dtype = _dtype_code(a, b)
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    elif out.dtype != torch.float32:
+        raise LaunchError(f"C dtype expected float32, got {str(out.dtype).replace('torch.', '')}")
+    if m == 0 or n == 0:
+        return out
+    if k > 0 and (a.stride(1) != 1 or (m > 1 and a.stride(0) < k)):
+        a = a.contiguous()
+    if k > 0 and (b.stride(1) != 1 or (k > 1 and b.stride(0) < n)):
+        b = b.contiguous()
+    direct = (out.stride(1) == 1 or n == 1) and (m == 1 or out.stride(0) >= n)
+    target = out if direct else torch.empty((m, n), dtype=torch.float32, device=a.device)
+    with torch.cuda.device(a.device):
+        stream = torch.cuda.current_stream(a.device).cuda_stream
+        _native.gemm(
+            algo,
+            dtype,
+            a.data_ptr(),
+            max(_row_stride(a), k),
+            b.data_ptr(),
+            max(_row_stride(b), n),
+            target.data_ptr(),
+            max(_row_stride(target), n),
+            m,
+            n,
+            k,
+            stream,
+        )
+    if target is not out:
+        out.copy_(target)
+    return out
+
+
+def library_path() -> str:
+    return _native.LIB_PATH
+
+
+def library_available() -> bool:
+    return os.path.exists(_native.LIB_PATH)
+
+
+__all__ = [
+    "Gfx950Target",
+    "KNOWN_GEMM_KERNELS",
+    "TARGET_NAME",
+    "find_lowering",
+    "gemm",
+    "launch",
+    "library_available",
+    "library_path",
+    "register_kernel",
+    "run",
+]

@@ -1,0 +1,112 @@
+"""ctypes binding of libhcg_gfx950.so (the C ABI in include/hcg_gemm.h).
+
+The library is built in-tree by 5_amd/csrc/build.py.  There is no fallback:
+if it is missing or cannot be loaded, every gfx950 launch raises
+``BackendError``.
+
+torch (when importable) is imported before the library is opened so that
+both share one HIP runtime: torch ships its own libamdhip64.so.7 and the
+dynamic loader reuses an already-loaded SONAME.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from .._errors import BackendError, LaunchError
+
+LIB_NAME = "libhcg_gfx950.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+HCG_OK = 0
+HCG_EINVAL = 1
+HCG_EHIP = 2
+
+HCG_F16 = 0
+HCG_BF16 = 1
+
+HCG_ALGO_AUTO = 0
+HCG_ALGO_TILED = 1
+HCG_ALGO_SKINNY = 2
+
+ALGOS = {"auto": HCG_ALGO_AUTO, "tiled": HCG_ALGO_TILED, "skinny": HCG_ALGO_SKINNY}
+
+# Every symbol include/hcg_gemm.h declares.
+EXPORTS = ("hcg_init", "hcg_gemm", "hcg_gemm_algo", "hcg_last_error", "hcg_version")
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    i64 = ctypes.c_int64
+    vp = ctypes.c_void_p
+    c_int = ctypes.c_int
+    lib.hcg_init.argtypes = []
+    lib.hcg_init.restype = c_int
+    lib.hcg_gemm.argtypes = [c_int, vp, i64, vp, i64, vp, i64, i64, i64, i64, vp]
+    lib.hcg_gemm.restype = c_int
+    lib.hcg_gemm_algo.argtypes = [c_int, c_int, vp, i64, vp, i64, vp, i64, i64, i64, i64, vp]
+    lib.hcg_gemm_algo.restype = c_int
+    lib.hcg_last_error.argtypes = []
+    lib.hcg_last_error.restype = ctypes.c_char_p
+    lib.hcg_version.argtypes = []
+    lib.hcg_version.restype = c_int
+
+
+def load() -> ctypes.CDLL:
+    """Open the library once (no device work happens here)."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise BackendError(
+                f"gfx950 backend library {LIB_PATH} is not built; run 5_amd/csrc/build.py"
+            )
+        try:
+            import torch  # noqa: F401  (share torch's HIP runtime)
+        except ImportError:
+            pass
+        try:
+            lib = ctypes.CDLL(LIB_PATH)
+        except OSError as exc:
+            raise BackendError(f"cannot load {LIB_PATH}: {exc}") from exc
+        _declare(lib)
+        _lib = lib
+        return lib
+
+
+def last_error(lib: ctypes.CDLL) -> str:
+    raw = lib.hcg_last_error()
+    return raw.decode("utf-8", "replace") if raw else ""
+
+
+def check(lib: ctypes.CDLL, rc: int, what: str) -> None:
+    if rc == HCG_OK:
+        return
+    msg = last_error(lib)
+    if rc == HCG_EINVAL:
+        raise LaunchError(f"{what}: {msg}")
+    raise BackendError(f"{what} failed ({rc}): {msg}")
+
+
+def gemm(
+    algo: int,
+    dtype: int,
+    a_ptr: int,
+    lda: int,
+    b_ptr: int,
+    ldb: int,
+    c_ptr: int,
+    ldc: int,
+    m: int,
+    n: int,
+    k: int,
+    stream: int,
+) -> None:
+    lib = load()
+    rc = lib.hcg_gemm_algo(algo, dtype, a_ptr, lda, b_ptr, ldb, c_ptr, ldc, m, n, k, stream or None)
+    check(lib, rc, "hcg_gemm")

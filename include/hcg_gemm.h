@@ -1,0 +1,80 @@
+/*
+ * hcg_gemm.h -- C ABI of the gfx950 (MI355X) backend for the hc tiled
+ * matrix-core GEMM.
+ *
+ * The reference (Hardcode84/5, the `hc` DSL) has no launch ABI: its only
+ * executable form of this kernel is the NumPy simulator, reached through
+ * `hc.simulator.launch(fn, *args, target=None)` (hc/simulator.py:165-186),
+ * and the future compiled entry `CompiledKernel.__call__`
+ * (hc/_compile.py:57-62) raises NotImplementedError.  These entry points are
+ * what that launch surface binds to on gfx950: plain pointers, sizes and a
+ * HIP stream; no framework types.
+ *
+ * Layouts (all row-major, as bound by the kernel's Buffer annotations
+ * `a: Buffer[M, K, f16]`, `b: Buffer[K, N, f16]`, `c: Buffer[M, N, f32]`,
+ * examples/amdgpu_gfx11_wmma_matmul.py:306-311):
+ *   A: M x K, element (i,k) at A[i*lda + k]
+ *   B: K x N, element (k,j) at B[k*ldb + j]
+ *   C: M x N float32, element (i,j) at C[i*ldc + j]
+ * A and B are 16-bit (fp16 or bf16, selected by `dtype`); accumulation is
+ * float32; C is written, never read, and only its M x N elements are
+ * touched (hc/simulator.py:1441-1458).
+ *
+ * Status codes: HCG_OK, HCG_EINVAL (argument rejected before any launch; the
+ * Python layer raises LaunchError), HCG_EHIP (a HIP runtime call failed; the
+ * text is in hcg_last_error()).  M == 0 or N == 0 is a no-op that launches
+ * nothing (hc/simulator.py:175-176); K == 0 writes zeros into C.
+ *
+ * All launches are asynchronous on `stream` (a hipStream_t; NULL = the
+ * null stream).  The entry points are re-entrant; error text is per thread.
+ */
+#ifndef HCG_GEMM_H
+#define HCG_GEMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HCG_OK 0
+#define HCG_EINVAL 1
+#define HCG_EHIP 2
+
+/* Operand element types. */
+#define HCG_F16 0
+#define HCG_BF16 1
+
+/* Kernel selection for hcg_gemm_algo. */
+#define HCG_ALGO_AUTO 0
+#define HCG_ALGO_TILED 1  /* 256x256 LDS-tiled MFMA kernel (compute-bound shapes) */
+#define HCG_ALGO_SKINNY 2 /* split-K streaming kernel for M <= 16 (HBM-bound shapes) */
+
+/* Idempotent one-time set-up (device properties).  Replaces the reference's
+ * once-per-process registration, lib/CAPI/HC.cpp:22-29.  Optional: every
+ * other entry point calls it. */
+int hcg_init(void);
+
+/* C = A @ B, the launch of `tiled_gfx11_wmma_matmul`
+ * (examples/amdgpu_gfx11_wmma_matmul.py:301-326) through
+ * hc.simulator.launch (hc/simulator.py:165-186).  Picks the kernel by shape. */
+int hcg_gemm(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, float* C,
+             int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Same as hcg_gemm with an explicit kernel choice (HCG_ALGO_*).  Used by
+ * tests and the benchmark to exercise each kernel; HCG_ALGO_SKINNY rejects
+ * M > 16 with HCG_EINVAL. */
+int hcg_gemm_algo(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
+                  float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Text of the calling thread's last error ("" if none). */
+const char* hcg_last_error(void);
+
+/* ABI version of this library (major * 100 + minor). */
+int hcg_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HCG_GEMM_H */

@@ -1,0 +1,265 @@
+"""CPU oracle for the hc tiled matrix-core GEMM -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import this module, and only as the checker (or the
+timed CPU baseline).  The product path under ``5_amd/`` never imports it.
+
+Semantics restated (reference citations):
+
+* ``wmma_gfx11`` fallback body, examples/amdgpu_gfx11_wmma_matmul.py:177-190:
+  per lane ``accum += np.float32(a_tile[r, k]) * np.float32(b_tile[k, col])``
+  for k in 0..15, on tiles whose inactive (out-of-bounds) entries were set to
+  +0 (``with_inactive``, :178-179, hc/_sim_types.py:353-357).
+* The accumulator starts at ``vzeros`` (:249-256) and is threaded through the
+  K loop in ascending ``k0`` (:315-324), so the whole launch is one strictly
+  sequential float32 fold per output element, k ascending, starting at +0.
+* Tile loads give masked-off payload 0 beyond M/N/K (hc/simulator.py:1338-1357)
+  and the store writes only the in-bounds part of C (hc/simulator.py:1441-1458).
+
+Parity pins for each function live in tests/test_oracle.py:
+
+* :func:`gemm_sequential` -- against a scalar ``np.float32`` triple loop
+  (brute force), against the reference's blocked-sum check within its own
+  ``atol=2e-6`` at the reference test shapes, against order-independent
+  integer known-answer tests (bit-exact), and against the float64 product
+  within the Higham bound ``gamma_K * (|A||B|)``.
+* :func:`gemm_c` (the C restatement, oracle/hc_oracle.c) -- bit-exact against
+  :func:`gemm_sequential` on random and ragged shapes for fp16 and bf16.
+* :func:`f32_to_bf16_bits` -- against torch's round-to-nearest-even cast and
+  hand-computed tie cases.
+* :func:`parity_check` -- its tolerance arithmetic is checked on planted
+  errors (a dropped k term, a transposed operand) that must fail.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libhc_oracle.so")
+
+F16 = 0
+BF16 = 1
+
+
+# --------------------------------------------------------------------------
+# bf16 helpers (numpy has no bfloat16; values travel as uint16 bit patterns)
+# --------------------------------------------------------------------------
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to bfloat16 (round-to-nearest-even) as uint16 bits.
+
+    NaN inputs are not expected (the generators draw finite values).
+    """
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return rounded.astype(np.uint16)
+
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def operand_to_f32(x: np.ndarray, dtype: int) -> np.ndarray:
+    if dtype == F16:
+        return np.asarray(x, dtype=np.float16).astype(np.float32)
+    return bf16_bits_to_f32(x)
+
+
+def operand_bits(x: np.ndarray, dtype: int) -> np.ndarray:
+    if dtype == F16:
+        return np.ascontiguousarray(x, dtype=np.float16).view(np.uint16)
+    return np.ascontiguousarray(x, dtype=np.uint16)
+
+
+# --------------------------------------------------------------------------
+# NumPy restatement
+# --------------------------------------------------------------------------
+
+
+def gemm_sequential(a: np.ndarray, b: np.ndarray, dtype: int = F16) -> np.ndarray:
+    """C = A @ B as one sequential float32 fold per element, k ascending.
+
+    Follows examples/amdgpu_gfx11_wmma_matmul.py:183-189 (the per-lane MAC),
+    :315-324 (ascending K loop) and :249-256 (zero-initialised accumulator).
+    Each step rounds the (exact) product and the sum to float32, exactly as
+    NumPy scalar float32 arithmetic does in the reference.
+    """
+    a32 = operand_to_f32(a, dtype)
+    b32 = operand_to_f32(b, dtype)
+    m, k = a32.shape
+    k2, n = b32.shape
+    if k != k2:
+        raise ValueError("A.shape[1] must match B.shape[0]")
+    acc = np.zeros((m, n), dtype=np.float32)
+    for kk in range(k):
+        prod = a32[:, kk : kk + 1] * b32[kk : kk + 1, :]  # float32, exact
+        acc += prod  # float32 round-to-nearest-even, elementwise
+    return acc
+
+
+def gemm_bruteforce(a: np.ndarray, b: np.ndarray, dtype: int = F16) -> np.ndarray:
+    """Scalar triple loop with ``np.float32`` scalars; tiny shapes only."""
+    a32 = operand_to_f32(a, dtype)
+    b32 = operand_to_f32(b, dtype)
+    m, k = a32.shape
+    _, n = b32.shape
+    out = np.zeros((m, n), dtype=np.float32)
+    for i in range(m):
+        for j in range(n):
+            s = np.float32(0.0)
+            for kk in range(k):
+                s = np.float32(s + np.float32(a32[i, kk]) * np.float32(b32[kk, j]))
+            out[i, j] = s
+    return out
+
+
+def gemm_blocked(a: np.ndarray, b: np.ndarray, dtype: int = F16, block: int = 16) -> np.ndarray:
+    """Sum over 16-wide K blocks of float32 matrix products.
+
+    This is the check the reference's own test applies to the simulator output
+    (tests/test_examples.py:23-33 with the helper at
+    examples/amdgpu_gfx11_wmma_matmul.py:329-335, ``atol=2e-6``); its
+    summation order differs from the simulator's, so it agrees only to that
+    tolerance.
+    """
+    a32 = operand_to_f32(a, dtype)
+    b32 = operand_to_f32(b, dtype)
+    out = np.zeros((a32.shape[0], b32.shape[1]), dtype=np.float32)
+    for k0 in range(0, a32.shape[1], block):
+        out += a32[:, k0 : k0 + block] @ b32[k0 : k0 + block, :]
+    return out
+
+
+# --------------------------------------------------------------------------
+# C restatement (oracle/hc_oracle.c) through ctypes
+# --------------------------------------------------------------------------
+
+_LIB = None
+
+
+def _lib():
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"oracle library {LIB_PATH} is not built; run oracle/build.py"
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        i64 = ctypes.c_int64
+        vp = ctypes.c_void_p
+        lib.hco_gemm.argtypes = [ctypes.c_int, vp, i64, vp, i64, vp, i64, i64, i64, i64, ctypes.c_int]
+        lib.hco_gemm.restype = ctypes.c_int
+        lib.hco_gemm_rows.argtypes = [
+            ctypes.c_int, vp, i64, vp, i64, i64, i64, i64, vp, i64, vp, ctypes.c_int
+        ]
+        lib.hco_gemm_rows.restype = ctypes.c_int
+        lib.hco_to_float.argtypes = [ctypes.c_int, vp, vp, i64]
+        lib.hco_to_float.restype = None
+        lib.hco_max_threads.argtypes = []
+        lib.hco_max_threads.restype = ctypes.c_int
+        _LIB = lib
+    return _LIB
+
+
+def available() -> bool:
+    return os.path.exists(LIB_PATH)
+
+
+def default_threads() -> int:
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        return int(env)
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def gemm_c(a: np.ndarray, b: np.ndarray, dtype: int = F16, threads: int | None = None) -> np.ndarray:
+    """Full C = A @ B from the C restatement (same bits as gemm_sequential)."""
+    ab = operand_bits(a, dtype)
+    bb = operand_bits(b, dtype)
+    m, k = ab.shape
+    k2, n = bb.shape
+    if k != k2:
+        raise ValueError("A.shape[1] must match B.shape[0]")
+    out = np.empty((m, n), dtype=np.float32)
+    rc = _lib().hco_gemm(
+        dtype, ab.ctypes.data, k, bb.ctypes.data, n, out.ctypes.data, n, m, n, k,
+        threads or default_threads(),
+    )
+    if rc != 0:
+        raise RuntimeError(f"hco_gemm failed with {rc}")
+    return out
+
+
+def gemm_c_rows(
+    a: np.ndarray, b: np.ndarray, rows: np.ndarray, dtype: int = F16, threads: int | None = None
+) -> np.ndarray:
+    """Rows ``rows`` of C = A @ B, shape (len(rows), N)."""
+    ab = operand_bits(a, dtype)
+    bb = operand_bits(b, dtype)
+    m, k = ab.shape
+    _, n = bb.shape
+    r = np.ascontiguousarray(rows, dtype=np.int64)
+    out = np.empty((r.size, n), dtype=np.float32)
+    rc = _lib().hco_gemm_rows(
+        dtype, ab.ctypes.data, k, bb.ctypes.data, n, m, n, k, r.ctypes.data, r.size,
+        out.ctypes.data, threads or default_threads(),
+    )
+    if rc != 0:
+        raise RuntimeError(f"hco_gemm_rows failed with {rc}")
+    return out
+
+
+def to_float_c(bits: np.ndarray, dtype: int) -> np.ndarray:
+    src = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(src.shape, dtype=np.float32)
+    _lib().hco_to_float(dtype, src.ctypes.data, out.ctypes.data, src.size)
+    return out
+
+
+# --------------------------------------------------------------------------
+# Parity criterion
+# --------------------------------------------------------------------------
+
+
+@dataclass
+class ParityReport:
+    rel_fro: float
+    max_abs: float
+    max_abs_bound: float
+    rel_fro_bound: float
+    ok: bool
+
+    def __str__(self) -> str:
+        return (
+            f"rel_fro={self.rel_fro:.3e} (<= {self.rel_fro_bound:.1e}) "
+            f"max|err|={self.max_abs:.3e} (<= {self.max_abs_bound:.3e}) ok={self.ok}"
+        )
+
+
+def max_abs_bound(k: int) -> float:
+    """max elementwise |err| <= 2e-2 * sqrt(K / 1024)."""
+    return 2e-2 * math.sqrt(max(k, 0) / 1024.0)
+
+
+def parity_check(got: np.ndarray, want: np.ndarray, k: int, rel_fro_bound: float = 1e-3) -> ParityReport:
+    """Relative Frobenius error <= 1e-3 and max |err| <= 2e-2*sqrt(K/1024)."""
+    g = np.asarray(got, dtype=np.float64)
+    w = np.asarray(want, dtype=np.float64)
+    if g.shape != w.shape:
+        raise ValueError(f"shape mismatch {g.shape} vs {w.shape}")
+    if not np.all(np.isfinite(g)):
+        return ParityReport(math.inf, math.inf, max_abs_bound(k), rel_fro_bound, False)
+    diff = g - w
+    denom = float(np.linalg.norm(w))
+    num = float(np.linalg.norm(diff))
+    rel = num / denom if denom > 0 else (0.0 if num == 0 else math.inf)
+    mx = float(np.max(np.abs(diff))) if diff.size else 0.0
+    bound = max_abs_bound(k)
+    return ParityReport(rel, mx, bound, rel_fro_bound, rel <= rel_fro_bound and mx <= bound)
