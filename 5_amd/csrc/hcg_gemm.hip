@@ -108,7 +108,7 @@ __device__ __forceinline__ void transpose8x8(const u32x4 (&in)[8], u32x4 (&out)[
 }
 
 // ---------------------------------------------------------------------------
-// Tiled kernel
+// Generic tiled kernel (global pointers; any alignment and size)
 // ---------------------------------------------------------------------------
 
 constexpr int kTileM = 256;
@@ -154,7 +154,7 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
 }
 
 template <int DT, bool kVecA, bool kVecB>
-__global__ __launch_bounds__(kTiledThreads) void gemm_tiled_kernel(TiledArgs g) {
+__global__ __launch_bounds__(kTiledThreads) void gemm_generic_kernel(TiledArgs g) {
   __shared__ u32x4 lds_a[2][kTileM * 8];
   __shared__ u32x4 lds_b[2][kTileN * 8];
 
@@ -260,6 +260,239 @@ __global__ __launch_bounds__(kTiledThreads) void gemm_tiled_kernel(TiledArgs g) 
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Fast tiled kernel (buffer loads; 16-byte aligned rows; offsets < 2^31)
+// ---------------------------------------------------------------------------
+
+struct FastArgs {
+  const uint16_t* A;
+  const uint16_t* B;
+  float* C;
+  int lda, ldb;  // elements; multiples of 8
+  int64_t ldc;
+  int M, N, K;
+  int tiles_m, tiles_n;
+  int a_bytes, b_bytes;  // buffer extents for the hardware range check
+};
+
+// Raw buffer resource: base, no swizzle/stride, `bytes` records.  Loads at or
+// beyond `bytes` return 0 (the hardware range check).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+
+// Mask keeping the first `valid` (clamped to [0, 8]) 16-bit lanes of a chunk.
+__device__ __forceinline__ u32x4 lane_mask(int valid) {
+  u32x4 m;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int lo = 2 * p;
+    m[p] = (valid > lo ? 0x0000ffffu : 0u) | (valid > lo + 1 ? 0xffff0000u : 0u);
+  }
+  return m;
+}
+
+// Scheduling-group masks for __builtin_amdgcn_sched_group_barrier.
+constexpr int kSgMfma = 0x008;
+constexpr int kSgVmemRead = 0x020;
+constexpr int kSgDsRead = 0x100;
+constexpr int kSgDsWrite = 0x200;
+constexpr int kSgValu = 0x002;
+
+// Interleave request for one block of 16 MFMAs: after each MFMA, up to one
+// DS read, one buffer load, one DS write and two VALU ops, while the counts
+// last (kSched == 1; kSched == 0 leaves scheduling to the compiler).
+template <int kSched, int kReads, int kVmem, int kWrites, int kValu>
+__device__ __forceinline__ void sched_hint() {
+  if constexpr (kSched == 1) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+      if constexpr (kReads > 0) if (i < kReads) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+      if constexpr (kVmem > 0) if (i < kVmem) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 1, 0);
+      if constexpr (kWrites > 0) if (i < kWrites) __builtin_amdgcn_sched_group_barrier(kSgDsWrite, 1, 0);
+      if constexpr (kValu > 0) if (2 * i < kValu) __builtin_amdgcn_sched_group_barrier(kSgValu, 2, 0);
+    }
+  }
+}
+
+template <int DT, int kSched>
+__global__ __launch_bounds__(kTiledThreads) void gemm_tiled_kernel(FastArgs g) {
+  __shared__ u32x4 lds_a[2][kTileM * 8];
+  __shared__ u32x4 lds_b[2][kTileN * 8];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int tm, tn;
+  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+  const int m0 = tm * kTileM, n0 = tn * kTileN;
+  const int nk = (g.K + kTileK - 1) / kTileK;
+  const bool k_tail = (g.K % kTileK) != 0;
+
+  const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(g.A, g.a_bytes);
+  const __amdgpu_buffer_rsrc_t rsrc_b = make_rsrc(g.B, g.b_bytes);
+
+  // Staging roles.  A: thread owns 16-byte chunk a_c of rows a_r + 32 i
+  // (8 lanes read one contiguous 128-byte row segment).  B: thread owns an
+  // 8(k) x 8(n) block at rows b_kb*8 + i, columns b_n*8 .. +7 (32 lanes read
+  // 512 contiguous bytes of a row); it is transposed in registers so LDS
+  // holds B as [n][k].  Rows past M (A) or K (B) lie beyond the buffer
+  // extent and load as 0; columns past N are masked once per thread.
+  const int a_c = tid & 7, a_r = tid >> 3;
+  const int b_n = tid & 31, b_kb = tid >> 5;
+  const int a_voff = ((m0 + a_r) * g.lda + a_c * 8) * 2;
+  const int a_step_i = 32 * g.lda * 2;
+  const int b_voff = ((b_kb * 8) * g.ldb + n0 + b_n * 8) * 2;
+  const int b_step_i = g.ldb * 2;
+  const u32x4 b_colmask = lane_mask(g.N - (n0 + b_n * 8));
+
+  u32x4 ga[8], gb[8];
+
+  // Global -> registers for K tile kt.  Every offset goes into the
+  // range-checked VGPR offset (the SGPR offset is not range-checked), so no
+  // load touches memory past the extent.
+  auto load_global = [&](int kt) {
+    const int k0 = kt * kTileK;
+    const int a_base = a_voff + k0 * 2;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ga[i] = buffer_load16(rsrc_a, a_base + i * a_step_i, 0);
+    const int b_base = b_voff + k0 * g.ldb * 2;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) gb[i] = buffer_load16(rsrc_b, b_base + i * b_step_i, 0);
+  };
+
+  // Registers -> LDS for K tile kt.  A columns >= K and B rows >= K (only in
+  // a partial last tile) and B columns >= N are zeroed by select, without
+  // branches; the masks are applied here, where the data is consumed, so the
+  // loads stay in flight until then.
+  auto store_lds = [&](int kt, int buf) {
+    const int k0 = kt * kTileK;
+    const u32x4 am = lane_mask(g.K - (k0 + a_c * 8));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) lds_a[buf][swz(a_r + 32 * i, a_c)] = ga[i] & am;
+    const int kr = g.K - (k0 + b_kb * 8);
+    u32x4 bm[8], bt[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) bm[i] = (i < kr) ? (gb[i] & b_colmask) : u32x4{0, 0, 0, 0};
+    transpose8x8(bm, bt);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) lds_b[buf][swz(b_n * 8 + n, b_kb)] = bt[n];
+  };
+
+  auto read_frags = [&](int buf, int kk, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
+    const int c = kk * 2 + (lane >> 5);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) fa[mi] = lds_a[buf][swz(wm * 128 + mi * 32 + (lane & 31), c)];
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) fb[ni] = lds_b[buf][swz(wn * 128 + ni * 32 + (lane & 31), c)];
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  auto mfma_block = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[4]) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma32x32x16<DT>(fa[mi], fb[ni], acc[mi][ni]);
+  };
+
+  u32x4 fa0[4], fb0[4], fa1[4], fb1[4];
+
+  load_global(0);
+  store_lds(0, 0);
+  __syncthreads();
+  read_frags(0, 0, fa0, fb0);
+
+  // Steady state: tile kt computes from LDS buffer kt&1 while tile kt+1 is
+  // loaded (block 0), transposed and written to the other buffer (block 2).
+  // Fragments for the next 16-wide K step are read while the current 16
+  // MFMAs run.  One barrier per tile, placed so the next tile's first
+  // fragments are read under the last MFMA block.
+  for (int kt = 0; kt + 1 < nk; ++kt) {
+    const int cur = kt & 1;
+    load_global(kt + 1);
+    read_frags(cur, 1, fa1, fb1);
+    mfma_block(fa0, fb0);
+    sched_hint<kSched, 8, 16, 0, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(cur, 2, fa0, fb0);
+    mfma_block(fa1, fb1);
+    sched_hint<kSched, 8, 0, 0, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(cur, 3, fa1, fb1);
+    store_lds(kt + 1, cur ^ 1);
+    mfma_block(fa0, fb0);
+    sched_hint<kSched, 8, 0, 16, 24>();
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    read_frags(cur ^ 1, 0, fa0, fb0);
+    mfma_block(fa1, fb1);
+    sched_hint<kSched, 8, 0, 0, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  {
+    const int cur = (nk - 1) & 1;
+    read_frags(cur, 1, fa1, fb1);
+    mfma_block(fa0, fb0);
+    read_frags(cur, 2, fa0, fb0);
+    mfma_block(fa1, fb1);
+    read_frags(cur, 3, fa1, fb1);
+    mfma_block(fa0, fb0);
+    mfma_block(fa1, fb1);
+  }
+
+  // Epilogue.  32x32 accumulator layout: register r of lane l holds
+  // row 8*(r/4) + 4*(l/32) + r%4, column l%32.  Only in-bounds C is written.
+  const int col_l = lane & 31;
+  const int row_l = (lane >> 5) * 4;
+  const bool full = (m0 + kTileM <= g.M) && (n0 + kTileN <= g.N);
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+      const int col = n0 + wn * 128 + ni * 32 + col_l;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 128 + mi * 32 + (r >> 2) * 8 + row_l + (r & 3);
+        if (full || (row < g.M && col < g.N)) g.C[(int64_t)row * g.ldc + col] = acc[mi][ni][r];
+      }
+    }
+  }
+}
+
+// Copy a rows x cols 16-bit matrix (row stride ld) into a zero-padded copy
+// with row stride ld_out (a multiple of 8), so the fast kernel can use
+// aligned 128-bit loads.  Columns [cols, ld_out) are written as 0.
+__global__ __launch_bounds__(256) void repack_kernel(const uint16_t* src, int64_t ld, int rows, int cols,
+                                                     uint16_t* dst, int ld_out) {
+  const int64_t chunks_per_row = ld_out / 8;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)rows * chunks_per_row) return;
+  const int row = (int)(idx / chunks_per_row);
+  const int c0 = (int)(idx % chunks_per_row) * 8;
+  const uint16_t* p = src + (int64_t)row * ld;
+  uint32_t w[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c = c0 + 2 * q;
+    const uint32_t lo = c < cols ? p[c] : 0u;
+    const uint32_t hi = c + 1 < cols ? p[c + 1] : 0u;
+    w[q] = lo | (hi << 16);
+  }
+  *reinterpret_cast<u32x4*>(dst + (int64_t)row * ld_out + c0) = u32x4{w[0], w[1], w[2], w[3]};
 }
 
 // ---------------------------------------------------------------------------
@@ -384,6 +617,7 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* C, int64_t ldc, i
   C[(idx / N) * ldc + (idx % N)] = 0.0f;
 }
 
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -408,6 +642,15 @@ int set_error(int code, const char* fmt, ...) {
   } while (0)
 
 constexpr int kMaxDevices = 64;
+constexpr int kMaxStreamWorkspaces = 16;
+
+// Library-owned scratch (split-K partials, repacked operands), one grow-only
+// buffer per (device, stream) so that concurrent streams never share it.
+struct Workspace {
+  void* stream = nullptr;
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
 
 struct DeviceState {
   std::once_flag once;
@@ -415,17 +658,18 @@ struct DeviceState {
   std::string init_error;
   int num_cus = 256;
   std::mutex ws_mutex;
-  float* ws = nullptr;
-  size_t ws_bytes = 0;
+  Workspace ws[kMaxStreamWorkspaces];
+  int ws_next = 0;
 };
 
 DeviceState g_devices[kMaxDevices];
-int g_skinny_splits_override = 0;
 std::once_flag g_global_once;
+int g_skinny_splits_override = 0;
+int g_tiled_sched = 1;
 
 void global_init() {
-  const char* s = getenv("HCG_SKINNY_SPLITS");
-  if (s) g_skinny_splits_override = atoi(s);
+  if (const char* s = getenv("HCG_SKINNY_SPLITS")) g_skinny_splits_override = atoi(s);
+  if (const char* s = getenv("HCG_TILED_SCHED")) g_tiled_sched = atoi(s);
 }
 
 int current_device_state(DeviceState** out) {
@@ -449,39 +693,67 @@ int current_device_state(DeviceState** out) {
   return HCG_OK;
 }
 
-// Library-owned split-K workspace, grown on demand and kept per device.
-int device_workspace(DeviceState* st, size_t bytes, float** out) {
+int stream_workspace(DeviceState* st, hipStream_t stream, size_t bytes, void** out) {
   std::lock_guard<std::mutex> lock(st->ws_mutex);
-  if (st->ws_bytes < bytes) {
-    if (st->ws) {
-      HCG_HIP_CHECK(hipDeviceSynchronize());
-      HCG_HIP_CHECK(hipFree(st->ws));
-      st->ws = nullptr;
-      st->ws_bytes = 0;
-    }
-    void* p = nullptr;
-    HCG_HIP_CHECK(hipMalloc(&p, bytes));
-    st->ws = static_cast<float*>(p);
-    st->ws_bytes = bytes;
+  Workspace* w = nullptr;
+  for (auto& cand : st->ws)
+    if (cand.ptr && cand.stream == (void*)stream) w = &cand;
+  if (!w) {
+    for (auto& cand : st->ws)
+      if (!cand.ptr) {
+        w = &cand;
+        break;
+      }
   }
-  *out = st->ws;
+  if (!w) {  // evict round-robin; hipFree waits for work that uses it
+    w = &st->ws[st->ws_next];
+    st->ws_next = (st->ws_next + 1) % kMaxStreamWorkspaces;
+  }
+  if (w->ptr && (w->stream != (void*)stream || w->bytes < bytes)) {
+    HCG_HIP_CHECK(hipFree(w->ptr));
+    w->ptr = nullptr;
+    w->bytes = 0;
+  }
+  if (!w->ptr) {
+    void* p = nullptr;
+    const size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    HCG_HIP_CHECK(hipMalloc(&p, want));
+    w->ptr = p;
+    w->bytes = want;
+  }
+  w->stream = (void*)stream;
+  *out = w->ptr;
   return HCG_OK;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 template <int DT>
-int launch_tiled(const TiledArgs& a, bool vec_a, bool vec_b, hipStream_t stream) {
+int launch_generic(const TiledArgs& a, bool vec_a, bool vec_b, hipStream_t stream) {
   const dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
   const dim3 block(kTiledThreads);
   if (vec_a && vec_b) {
-    gemm_tiled_kernel<DT, true, true><<<grid, block, 0, stream>>>(a);
+    gemm_generic_kernel<DT, true, true><<<grid, block, 0, stream>>>(a);
   } else if (vec_a) {
-    gemm_tiled_kernel<DT, true, false><<<grid, block, 0, stream>>>(a);
+    gemm_generic_kernel<DT, true, false><<<grid, block, 0, stream>>>(a);
   } else if (vec_b) {
-    gemm_tiled_kernel<DT, false, true><<<grid, block, 0, stream>>>(a);
+    gemm_generic_kernel<DT, false, true><<<grid, block, 0, stream>>>(a);
   } else {
-    gemm_tiled_kernel<DT, false, false><<<grid, block, 0, stream>>>(a);
+    gemm_generic_kernel<DT, false, false><<<grid, block, 0, stream>>>(a);
+  }
+  HCG_HIP_CHECK(hipGetLastError());
+  return HCG_OK;
+}
+
+template <int DT>
+int launch_fast(const FastArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
+  const dim3 block(kTiledThreads);
+  if (g_tiled_sched == 0) {
+    gemm_tiled_kernel<DT, 0><<<grid, block, 0, stream>>>(a);
+  } else {
+    gemm_tiled_kernel<DT, 1><<<grid, block, 0, stream>>>(a);
   }
   HCG_HIP_CHECK(hipGetLastError());
   return HCG_OK;
@@ -527,11 +799,127 @@ int skinny_splits(const DeviceState* st, int N, int K) {
   return splits;
 }
 
+int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
+               float* C, int64_t ldc, int M, int N, int K, hipStream_t stream) {
+  SkinnyArgs a{};
+  a.A = static_cast<const uint16_t*>(A);
+  a.B = static_cast<const uint16_t*>(B);
+  a.C = C;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.ldc = ldc;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.splits = skinny_splits(st, N, K);
+  const int kunit = kSkinnyStep * kSkinnyWaves;
+  const int kunits = (K + kunit - 1) / kunit;
+  a.kchunk = ((kunits + a.splits - 1) / a.splits) * kunit;
+  a.splits = (K + a.kchunk - 1) / a.kchunk;  // drop empty trailing splits
+  a.ws = nullptr;
+  if (a.splits > 1) {
+    void* ws = nullptr;
+    const int rc = stream_workspace(st, stream, (size_t)a.splits * 16 * (size_t)N * sizeof(float), &ws);
+    if (rc != HCG_OK) return rc;
+    a.ws = static_cast<float*>(ws);
+  }
+  const bool vec_a = aligned16(A) && (lda % 8 == 0);
+  const bool vec_b = aligned16(B) && (ldb % 8 == 0);
+  return dtype == HCG_F16 ? launch_skinny<HCG_F16>(a, vec_a, vec_b, stream)
+                          : launch_skinny<HCG_BF16>(a, vec_a, vec_b, stream);
+}
+
+int run_generic(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, float* C,
+                int64_t ldc, int M, int N, int K, hipStream_t stream) {
+  TiledArgs a{};
+  a.A = static_cast<const uint16_t*>(A);
+  a.B = static_cast<const uint16_t*>(B);
+  a.C = C;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.ldc = ldc;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.tiles_m = (M + kTileM - 1) / kTileM;
+  a.tiles_n = (N + kTileN - 1) / kTileN;
+  if ((int64_t)a.tiles_m * a.tiles_n > 0x7fffffff) return set_error(HCG_EINVAL, "too many output tiles");
+  const bool vec_a = aligned16(A) && (lda % 8 == 0);
+  const bool vec_b = aligned16(B) && (ldb % 8 == 0);
+  return dtype == HCG_F16 ? launch_generic<HCG_F16>(a, vec_a, vec_b, stream)
+                          : launch_generic<HCG_BF16>(a, vec_a, vec_b, stream);
+}
+
+// Largest byte offset the fast kernel forms for A (rows up to the padded tile
+// extent) or B (rows up to the padded K extent); must stay below 2^31.
+int64_t fast_extent_a(int M, int K, int64_t lda) {
+  return ((int64_t)round_up(M, kTileM) * lda + round_up(K, kTileK) + 8) * 2;
+}
+int64_t fast_extent_b(int N, int K, int64_t ldb) {
+  return ((int64_t)round_up(K, kTileK) * ldb + round_up(N, kTileN) + 8) * 2;
+}
+
+int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
+              float* C, int64_t ldc, int M, int N, int K, hipStream_t stream, bool force_generic) {
+  const int64_t kLimit = (int64_t)1 << 31;
+  const bool a_ok = aligned16(A) && lda % 8 == 0;
+  const bool b_ok = aligned16(B) && ldb % 8 == 0;
+  const int64_t lda_p = a_ok ? lda : (int64_t)round_up(K, 8);
+  const int64_t ldb_p = b_ok ? ldb : (int64_t)round_up(N, 8);
+  const int64_t tiles = (int64_t)((M + kTileM - 1) / kTileM) * ((N + kTileN - 1) / kTileN);
+  const bool fits = fast_extent_a(M, K, lda_p) < kLimit && fast_extent_b(N, K, ldb_p) < kLimit &&
+                    tiles <= 0x7fffffff;
+  if (force_generic || !fits) return run_generic(dtype, A, lda, B, ldb, C, ldc, M, N, K, stream);
+
+  const uint16_t* a_use = static_cast<const uint16_t*>(A);
+  const uint16_t* b_use = static_cast<const uint16_t*>(B);
+  if (!a_ok || !b_ok) {
+    // Unaligned rows: repack into zero-padded, 16-byte aligned copies.
+    const size_t a_sz = a_ok ? 0 : round_up((size_t)M * lda_p * 2, 256);
+    const size_t b_sz = b_ok ? 0 : round_up((size_t)K * ldb_p * 2, 256);
+    void* ws = nullptr;
+    const int rc = stream_workspace(st, stream, a_sz + b_sz, &ws);
+    if (rc != HCG_OK) return rc;
+    uint16_t* a_p = static_cast<uint16_t*>(ws);
+    uint16_t* b_p = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + a_sz);
+    if (!a_ok) {
+      const int64_t n = (int64_t)M * (lda_p / 8);
+      repack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(a_use, lda, M, K, a_p, (int)lda_p);
+      HCG_HIP_CHECK(hipGetLastError());
+      a_use = a_p;
+    }
+    if (!b_ok) {
+      const int64_t n = (int64_t)K * (ldb_p / 8);
+      repack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(b_use, ldb, K, N, b_p, (int)ldb_p);
+      HCG_HIP_CHECK(hipGetLastError());
+      b_use = b_p;
+    }
+  }
+  FastArgs f{};
+  f.A = a_use;
+  f.B = b_use;
+  f.C = C;
+  f.lda = (int)lda_p;
+  f.ldb = (int)ldb_p;
+  f.ldc = ldc;
+  f.M = M;
+  f.N = N;
+  f.K = K;
+  f.tiles_m = (M + kTileM - 1) / kTileM;
+  f.tiles_n = (N + kTileN - 1) / kTileN;
+  // Range-check extents cover the last valid element, rounded up to the
+  // 16-byte chunk that holds it (never past that chunk).
+  f.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda_p + K) * 2, 16);
+  f.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * ldb_p + N) * 2, 16);
+  return dtype == HCG_F16 ? launch_fast<HCG_F16>(f, stream) : launch_fast<HCG_BF16>(f, stream);
+}
+
 int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
               float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream_ptr) {
   if (dtype != HCG_F16 && dtype != HCG_BF16)
     return set_error(HCG_EINVAL, "dtype must be HCG_F16 (0) or HCG_BF16 (1), got %d", dtype);
-  if (algo != HCG_ALGO_AUTO && algo != HCG_ALGO_TILED && algo != HCG_ALGO_SKINNY)
+  if (algo != HCG_ALGO_AUTO && algo != HCG_ALGO_TILED && algo != HCG_ALGO_SKINNY &&
+      algo != HCG_ALGO_GENERIC)
     return set_error(HCG_EINVAL, "unknown algo %d", algo);
   if (M < 0 || N < 0 || K < 0)
     return set_error(HCG_EINVAL, "negative extent: M=%lld N=%lld K=%lld", (long long)M,
@@ -566,50 +954,12 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
     return HCG_OK;
   }
 
-  const bool vec_a = aligned16(A) && (lda % 8 == 0);
-  const bool vec_b = aligned16(B) && (ldb % 8 == 0);
   const bool use_skinny = algo == HCG_ALGO_SKINNY || (algo == HCG_ALGO_AUTO && M <= 16);
-
   if (use_skinny) {
-    SkinnyArgs a{};
-    a.A = static_cast<const uint16_t*>(A);
-    a.B = static_cast<const uint16_t*>(B);
-    a.C = C;
-    a.lda = lda;
-    a.ldb = ldb;
-    a.ldc = ldc;
-    a.M = (int)M;
-    a.N = (int)N;
-    a.K = (int)K;
-    a.splits = skinny_splits(st, (int)N, (int)K);
-    const int kunit = kSkinnyStep * kSkinnyWaves;
-    const int kunits = ((int)K + kunit - 1) / kunit;
-    a.kchunk = ((kunits + a.splits - 1) / a.splits) * kunit;
-    a.splits = ((int)K + a.kchunk - 1) / a.kchunk;  // drop empty trailing splits
-    a.ws = nullptr;
-    if (a.splits > 1) {
-      rc = device_workspace(st, (size_t)a.splits * 16 * (size_t)N * sizeof(float), &a.ws);
-      if (rc != HCG_OK) return rc;
-    }
-    rc = dtype == HCG_F16 ? launch_skinny<HCG_F16>(a, vec_a, vec_b, stream)
-                          : launch_skinny<HCG_BF16>(a, vec_a, vec_b, stream);
+    rc = run_skinny(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream);
   } else {
-    TiledArgs a{};
-    a.A = static_cast<const uint16_t*>(A);
-    a.B = static_cast<const uint16_t*>(B);
-    a.C = C;
-    a.lda = lda;
-    a.ldb = ldb;
-    a.ldc = ldc;
-    a.M = (int)M;
-    a.N = (int)N;
-    a.K = (int)K;
-    a.tiles_m = (int)((M + kTileM - 1) / kTileM);
-    a.tiles_n = (int)((N + kTileN - 1) / kTileN);
-    if ((int64_t)a.tiles_m * a.tiles_n > 0x7fffffff)
-      return set_error(HCG_EINVAL, "too many output tiles");
-    rc = dtype == HCG_F16 ? launch_tiled<HCG_F16>(a, vec_a, vec_b, stream)
-                          : launch_tiled<HCG_BF16>(a, vec_a, vec_b, stream);
+    rc = run_tiled(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream,
+                   algo == HCG_ALGO_GENERIC);
   }
   if (rc == HCG_OK) t_last_error.clear();
   return rc;

@@ -30,8 +30,9 @@ HCG_BF16 = 1
 HCG_ALGO_AUTO = 0
 HCG_ALGO_TILED = 1
 HCG_ALGO_SKINNY = 2
+HCG_ALGO_GENERIC = 3
 
-ALGOS = {"auto": HCG_ALGO_AUTO, "tiled": HCG_ALGO_TILED, "skinny": HCG_ALGO_SKINNY}
+ALGOS = {"auto": HCG_ALGO_AUTO, "tiled": HCG_ALGO_TILED, "skinny": HCG_ALGO_SKINNY, "generic": HCG_ALGO_GENERIC}
 
 # Every symbol include/hcg_gemm.h declares.
 EXPORTS = ("hcg_init", "hcg_gemm", "hcg_gemm_algo", "hcg_last_error", "hcg_version")

@@ -1,0 +1,258 @@
+"""Benchmark of the hc GEMM hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+                    [--no-cpu-baseline] [--no-extra]
+
+A step is one launch of the GEMM C = A @ B over the workload's synthetic
+inputs (already resident in HBM).  The headline workload is BASELINE.json's
+metric configuration, fp16 M=N=K=4096; ``value`` is TFLOP/s
+(2*M*N*K per step).  One JSON line is printed with:
+
+* ``roofline``: the dominant kernel's algorithmic flops per launch divided by
+  its average launch time (HIP events on the launch stream, over the timed
+  region), against MI355X's dense fp16 MFMA peak (2516.6 TFLOP/s = 256 CUs x
+  2.4 GHz x 4096 flop/clk/CU);
+* ``cpu_baseline``: the C oracle (the reference simulator's float32 fold,
+  restated; OpenMP) timed on this host on a bounded sample of rows of the
+  same workload (kind "port");
+* ``skinny``: the M=16 decode-shaped GEMM in GB/s of algorithmic
+  bytes against the 8 TB/s HBM peak, timed while rotating through enough
+  copies of B that every launch streams B from HBM, not from the 256 MB
+  Infinity Cache (warm, same-buffer numbers are reported beside it);
+* ``others``: the remaining BASELINE.json configurations, TFLOP/s.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "5_amd"))
+
+PEAK_F16_TFLOPS = 2516.6  # dense fp16/bf16 MFMA, MI355X
+PEAK_HBM_GBS = 8000.0
+METRIC = "TFLOP/s + % MFMA fp16 peak at 4096³ GEMM; GB/s at M=16 skinny, 1 MI355X"
+MALL_BYTES = 256 * 1024 * 1024
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse_args() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--workload", default="c2_4096_f16")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extra", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU time of the baseline sample")
+    return p.parse_args()
+
+
+def dtype_short(name: str) -> str:
+    return {"float16": "f16", "bfloat16": "bf16"}[name]
+
+
+def time_launches(torch, stream, fn, steps: int, warmup: int) -> tuple[float, float]:
+    """(event seconds per launch, host seconds per step) over `steps` launches."""
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        end.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return start.elapsed_time(end) * 1e-3 / steps, (t1 - t0) / steps
+
+
+def cpu_baseline(cfg, a, b, target_s: float) -> dict:
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+
+    import hc_oracle
+
+    threads = hc_oracle.default_threads()
+    dt = hc_oracle.F16 if cfg.dtype == "float16" else hc_oracle.BF16
+    rows = 16
+    elapsed = 0.0
+    while True:
+        idx = np.arange(rows, dtype=np.int64)
+        t0 = time.perf_counter()
+        hc_oracle.gemm_c_rows(a, b, idx, dt, threads=threads)
+        elapsed = time.perf_counter() - t0
+        if elapsed >= target_s / 4 or rows >= cfg.m:
+            break
+        rows = min(cfg.m, max(rows * 2, int(rows * (target_s / 4) / max(elapsed, 1e-3))))
+    # One more run at the size that lands near the target, timed as the result.
+    rows = min(cfg.m, max(16, int(rows * target_s / max(elapsed, 1e-3) / 2)))
+    idx = np.arange(rows, dtype=np.int64)
+    t0 = time.perf_counter()
+    hc_oracle.gemm_c_rows(a, b, idx, dt, threads=threads)
+    elapsed = time.perf_counter() - t0
+    flops = 2.0 * rows * cfg.n * cfg.k
+    return {
+        "value": flops / elapsed / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"rows 0..{rows - 1} of {cfg.name} ({rows}x{cfg.n}x{cfg.k}), {elapsed:.1f} s, "
+        f"C oracle (sequential fp32 fold, OpenMP over row blocks) on {os.cpu_count()} host CPUs",
+    }
+
+
+def bench_skinny(torch, g, stream, steps: int, warmup: int) -> dict:
+    from hc.gfx950.workloads import CONFIGS, make_inputs, to_torch
+
+    cfg = CONFIGS["c4_skinny_f16"]
+    dev = torch.device("cuda", 0)
+    a, b = make_inputs(cfg, seed=0)
+    ta = to_torch(a, cfg.dtype, dev)
+    tb0 = to_torch(b, cfg.dtype, dev)
+    copies = max(3, math.ceil(2 * MALL_BYTES / tb0.numel() / 2) + 1)
+    tbs = [tb0] + [tb0.clone() for _ in range(copies - 1)]
+    tc = torch.empty((cfg.m, cfg.n), dtype=torch.float32, device=dev)
+    it = {"i": 0}
+
+    def rotating():
+        tb = tbs[it["i"] % copies]
+        it["i"] += 1
+        g.gemm(ta, tb, out=tc, algo="skinny")
+
+    cold, _ = time_launches(torch, stream, rotating, steps, warmup)
+    warm, _ = time_launches(torch, stream, lambda: g.gemm(ta, tb0, out=tc, algo="skinny"), steps, warmup)
+    gbs = cfg.algorithmic_bytes / cold / 1e9
+    return {
+        "workload": cfg.name,
+        "M": cfg.m,
+        "N": cfg.n,
+        "K": cfg.k,
+        "value": gbs,
+        "unit": "GB/s",
+        "us_per_launch": cold * 1e6,
+        "frac_hbm_peak": gbs / PEAK_HBM_GBS,
+        "algorithmic_bytes": cfg.algorithmic_bytes,
+        "b_copies_rotated": copies,
+        "warm_same_buffer_GBs": cfg.algorithmic_bytes / warm / 1e9,
+        "note": "time per launch includes the split-K reduce kernel",
+    }
+
+
+def bench_config(torch, g, stream, name: str, steps: int, warmup: int) -> dict:
+    from hc.gfx950.workloads import CONFIGS, make_inputs, to_torch
+
+    cfg = CONFIGS[name]
+    dev = torch.device("cuda", 0)
+    a, b = make_inputs(cfg, seed=0)
+    ta, tb = to_torch(a, cfg.dtype, dev), to_torch(b, cfg.dtype, dev)
+    tc = torch.empty((cfg.m, cfg.n), dtype=torch.float32, device=dev)
+    t, _ = time_launches(torch, stream, lambda: g.gemm(ta, tb, out=tc), steps, warmup)
+    tf = cfg.flops / t / 1e12
+    return {"value": tf, "unit": "TFLOP/s", "us_per_launch": t * 1e6, "frac_peak": tf / PEAK_F16_TFLOPS}
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X; "
+            "the GEMM shards by N or M with no exchange (see DESIGN.md), and no multi-GPU run is part of it",
+            file=sys.stderr,
+        )
+        return 2
+    import torch
+
+    import hc.gfx950 as g
+    from hc.gfx950.workloads import CONFIGS, make_inputs, to_torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    cfg = CONFIGS[args.workload]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(device=dev)
+    log(f"bench: {torch.cuda.get_device_name(0)}, workload {cfg.name}")
+
+    a, b = make_inputs(cfg, seed=0)
+    ta, tb = to_torch(a, cfg.dtype, dev), to_torch(b, cfg.dtype, dev)
+    tc = torch.empty((cfg.m, cfg.n), dtype=torch.float32, device=dev)
+
+    def step():
+        g.gemm(ta, tb, out=tc)
+
+    per_launch, host_per_step = time_launches(torch, stream, step, args.steps, args.warmup)
+    tflops = cfg.flops / per_launch / 1e12
+    log(f"bench: {cfg.name}: {per_launch * 1e6:.1f} us/launch, {tflops:.1f} TFLOP/s")
+    is_skinny = cfg.m <= 16
+    kernel_name = "gemm_skinny_kernel" if is_skinny else "gemm_tiled_kernel"
+    if is_skinny:
+        achieved = cfg.algorithmic_bytes / per_launch / 1e9
+        roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": achieved / PEAK_HBM_GBS, "traffic": None}
+    else:
+        roofline = {"bound": "mfma", "achieved": tflops, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                    "frac": tflops / PEAK_F16_TFLOPS, "traffic": None}
+    roofline["kernel"] = kernel_name
+    roofline["per_launch_us"] = per_launch * 1e6
+    roofline["algorithmic_per_launch"] = cfg.algorithmic_bytes if is_skinny else cfg.flops
+
+    result = {
+        "metric": METRIC,
+        "value": tflops,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": host_per_step * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype_short(cfg.dtype),
+        "data": "synthetic",
+        "config": {
+            "workload": cfg.name,
+            "M": cfg.m,
+            "N": cfg.n,
+            "K": cfg.k,
+            "inputs": f"{cfg.dtype}, A~{cfg.a_dist}, B~{cfg.b_dist}, seed 0",
+            "accumulate": "f32",
+            "output": "f32",
+            "layout": "row-major A (MxK), B (KxN), C (MxN)",
+        },
+        "pct_mfma_fp16_peak": 100.0 * tflops / PEAK_F16_TFLOPS,
+        "roofline": roofline,
+    }
+    del ta, tb, tc
+    if not args.no_extra:
+        log("bench: skinny M=16 (rotating B buffers)")
+        result["skinny"] = bench_skinny(torch, g, stream, max(20, args.steps), max(5, args.warmup // 2))
+        others = {}
+        for name in CONFIGS:
+            if name in (cfg.name, "c4_skinny_f16"):
+                continue
+            log(f"bench: {name}")
+            others[name] = bench_config(torch, g, stream, name, max(10, args.steps // 4), 5)
+        result["others"] = others
+    if not args.no_cpu_baseline:
+        log("bench: CPU baseline (oracle)")
+        result["cpu_baseline"] = cpu_baseline(cfg, a, b, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -49,6 +49,7 @@ extern "C" {
 #define HCG_ALGO_AUTO 0
 #define HCG_ALGO_TILED 1  /* 256x256 LDS-tiled MFMA kernel (compute-bound shapes) */
 #define HCG_ALGO_SKINNY 2 /* split-K streaming kernel for M <= 16 (HBM-bound shapes) */
+#define HCG_ALGO_GENERIC 3 /* pointer-based tiled kernel: any alignment and size (fallback) */
 
 /* Idempotent one-time set-up (device properties).  Replaces the reference's
  * once-per-process registration, lib/CAPI/HC.cpp:22-29.  Optional: every
