@@ -32,6 +32,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <type_traits>
 #include <string>
 
 #include "hcg_gemm.h"
@@ -275,6 +276,7 @@ struct FastArgs {
   int M, N, K;
   int tiles_m, tiles_n;
   int a_bytes, b_bytes;  // buffer extents for the hardware range check
+  bool c_vec;            // C rows are 16-byte aligned at every 4th column
 };
 
 // Raw buffer resource: base, no swizzle/stride, `bytes` records.  Loads at or
@@ -473,6 +475,295 @@ __global__ __launch_bounds__(kTiledThreads) void gemm_tiled_kernel(FastArgs g) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// DMA tiled kernel: global -> LDS with buffer_load ... lds (no VGPR staging)
+// ---------------------------------------------------------------------------
+//
+// 256x256 output tile, 4 waves (2x2, 128x128 each, 4x4 MFMA 32x32x16), K step
+// 32, and a 4-stage LDS ring: tile kt+3 is requested while tile kt is being
+// multiplied, so each load has about three tiles of MFMA time to land.
+//
+// Stage layout (32 KB): A as [256 rows][32 k] (64-byte rows of 4 chunks of
+// 16 bytes), B as [32 k][256 n] (512-byte rows of 32 chunks); chunks are
+// XOR-swizzled per row (a_chunk_swz, b_chunk_swz).  A fragments are one ds_read_b128;
+// B fragments are two ds_read_b64_tr_b16, which within each 16-lane group
+// hand lane i element i%4 of source lane 4j + i/4 (j = 0..3): source lanes
+// point at 4 consecutive k rows x 16 columns, so lane i receives 4
+// consecutive k of column i, the MFMA B operand.
+//
+// Requirements (checked on the host): A, B 16-byte aligned; lda, ldb, K, N
+// multiples of 8 (or operands repacked to that form with zero padding).
+// Chunks past K or N are redirected past the buffer extent, so the hardware
+// range check returns zeros; rows past M (A) or K (B) are past it already.
+
+constexpr int kDmaK = 32;
+constexpr int kDmaStages = 4;
+constexpr int kDmaStageBytes = (kTileM + kTileN) * kDmaK * 2;  // 32 KB
+constexpr int kOobOffset = 0x7ffffff0;
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt with only vmcnt (lgkmcnt / expcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, lds_void* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, 0, 0, 0);
+}
+
+// The four stages are separate LDS objects and every access names its stage
+// at compile time, so the compiler can tell a DMA into one stage from reads
+// of another and does not serialize them with a full vmcnt wait.
+__shared__ __attribute__((aligned(1024))) unsigned char g_stage0[kDmaStageBytes];
+__shared__ __attribute__((aligned(1024))) unsigned char g_stage1[kDmaStageBytes];
+__shared__ __attribute__((aligned(1024))) unsigned char g_stage2[kDmaStageBytes];
+__shared__ __attribute__((aligned(1024))) unsigned char g_stage3[kDmaStageBytes];
+
+template <int S>
+__device__ __forceinline__ unsigned char* dma_stage() {
+  if constexpr (S == 0) return g_stage0;
+  else if constexpr (S == 1) return g_stage1;
+  else if constexpr (S == 2) return g_stage2;
+  else return g_stage3;
+}
+
+template <int S>
+using StageC = std::integral_constant<int, S>;
+
+// Physical 16-byte chunk of logical chunk c in A row `row` (4 chunks/row).
+// 16 consecutive rows read at one chunk land on 16 distinct 16-byte bank
+// groups (64 banks), and any 8 consecutive rows on 8 (32 banks).
+__device__ __forceinline__ int a_chunk_swz(int row, int c) {
+  return c ^ ((row >> 1) & 3) ^ ((row >> 3) & 1);
+}
+
+// Physical chunk of logical chunk c in B row k (32 chunks/row).  A 32-lane
+// transposed read touches 4 consecutive k rows x 4 consecutive chunks; the
+// XOR pattern {0, 4, 10, 14} makes those 16 accesses distinct modulo 16
+// (64 banks) and each 16-lane half distinct modulo 8 (32 banks).
+__device__ __forceinline__ int b_chunk_swz(int k, int c) {
+  const int m = k & 3;
+  return c ^ ((m >> 1) * 10 + (m & 1) * 4);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kTiledThreads) void gemm_dma_kernel(FastArgs g) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  // Wave index as a provably uniform value: it feeds the LDS base (M0) of
+  // the DMA loads.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int tm, tn;
+  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+  const int m0 = tm * kTileM, n0 = tn * kTileN;
+  const int nk = (g.K + kDmaK - 1) / kDmaK;
+
+  const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(g.A, g.a_bytes);
+  const __amdgpu_buffer_rsrc_t rsrc_b = make_rsrc(g.B, g.b_bytes);
+
+  // DMA roles.  Each wave instruction fills 1 KB of LDS, lane l at byte
+  // 16*l.  A: wave w owns 16-row blocks 4w..4w+3; lane l covers row
+  // blk*16 + l/4 at physical chunk l%4, so it loads the logical chunk that
+  // the swizzle puts there (the swizzles are XOR involutions).  B: wave w
+  // owns 2-row blocks 4w..4w+3; lane l covers k row blk*2 + l/32 at
+  // physical chunk l%32.
+  int a_off[4], a_col[4], b_off[4], b_row[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int blk = wave * 4 + i;
+    const int row = blk * 16 + (lane >> 2);
+    const int c = a_chunk_swz(row, lane & 3);
+    a_col[i] = c * 8;
+    a_off[i] = ((m0 + row) * g.lda + c * 8) * 2;
+    const int kr = blk * 2 + (lane >> 5);
+    const int cb = b_chunk_swz(kr, lane & 31);
+    // Columns past N never change with k: push such a chunk's row out of
+    // range once so the per-tile row test also covers them.
+    b_row[i] = (n0 + cb * 8 < g.N) ? kr : 0x3fffffff;
+    b_off[i] = (kr * g.ldb + n0 + cb * 8) * 2;
+  }
+
+  auto issue_tile = [&](auto sc, int kt) {
+    unsigned char* st = dma_stage<decltype(sc)::value>();
+    const int k0 = kt * kDmaK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int off = (k0 + a_col[i] < g.K) ? a_off[i] + k0 * 2 : kOobOffset;
+      dma16(rsrc_a, (lds_void*)(st + (wave * 4 + i) * 1024), off);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int off = (k0 + b_row[i] < g.K) ? b_off[i] + k0 * g.ldb * 2 : kOobOffset;
+      dma16(rsrc_b, (lds_void*)(st + kTileM * kDmaK * 2 + (wave * 4 + i) * 1024), off);
+    }
+  };
+
+  // Fragment addresses (bytes within a stage).
+  int fa_addr[2][4], fb_addr[2][4][2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      const int row = wm * 128 + mi * 32 + (lane & 31);
+      const int c = kk * 2 + (lane >> 5);
+      fa_addr[kk][mi] = row * 64 + a_chunk_swz(row, c) * 16;
+    }
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int sl = lane & 15, grp = lane >> 4;
+        const int krow = kk * 16 + 8 * (grp >> 1) + 4 * h + (sl >> 2);
+        const int ncol = wn * 128 + ni * 32 + 16 * (grp & 1) + 4 * (sl & 3);
+        const int c = ncol >> 3;
+        fb_addr[kk][ni][h] = kTileM * kDmaK * 2 + krow * 512 + b_chunk_swz(krow, c) * 16 + (ncol & 7) * 2;
+      }
+    }
+  }
+
+  auto read_frags = [&](auto sc, int kk, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
+    const unsigned char* st = dma_stage<decltype(sc)::value>();
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) fa[mi] = *reinterpret_cast<const u32x4*>(st + fa_addr[kk][mi]);
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(st + fb_addr[kk][ni][0]));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(st + fb_addr[kk][ni][1]));
+      const uint64_t l64 = __builtin_bit_cast(uint64_t, lo), h64 = __builtin_bit_cast(uint64_t, hi);
+      fb[ni] = u32x4{(uint32_t)l64, (uint32_t)(l64 >> 32), (uint32_t)h64, (uint32_t)(h64 >> 32)};
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  auto mfma_block = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[4]) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma32x32x16<DT>(fa[mi], fb[ni], acc[mi][ni]);
+  };
+
+  u32x4 fa0[4], fb0[4], fa1[4], fb1[4];
+
+  // One K tile from stage S.  On entry fa0/fb0 hold its first 16-wide K
+  // step; on exit they hold the next tile's.
+  auto iteration = [&](auto sc, int kt) {
+    constexpr int S = decltype(sc)::value;
+    read_frags(sc, 1, fa1, fb1);
+    mfma_block(fa0, fb0);
+    // Issue the 12 fragment reads early, between the first MFMAs.
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSgMfma, 10, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // Tile kt+1 has landed for this wave (tile kt+2 may still be in flight);
+    // this wave's fragment reads of tile kt are complete.
+    wait_vmcnt<8>();
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    // Every wave is past its reads of tile kt-1: its stage takes tile kt+3
+    // (tiles past K load zeros and are never multiplied).
+    issue_tile(StageC<(S + 3) & 3>{}, kt + 3);
+    read_frags(StageC<(S + 1) & 3>{}, 0, fa0, fb0);
+    mfma_block(fa1, fb1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 1, 0);
+      if (i < 6) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSgMfma, 8, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Prologue: tiles 0..2 in flight.
+  issue_tile(StageC<0>{}, 0);
+  issue_tile(StageC<1>{}, 1);
+  issue_tile(StageC<2>{}, 2);
+  wait_vmcnt<16>();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  read_frags(StageC<0>{}, 0, fa0, fb0);
+
+  int kt = 0;
+  for (; kt + 4 <= nk; kt += 4) {
+    iteration(StageC<0>{}, kt);
+    iteration(StageC<1>{}, kt + 1);
+    iteration(StageC<2>{}, kt + 2);
+    iteration(StageC<3>{}, kt + 3);
+  }
+  if (kt < nk) iteration(StageC<0>{}, kt++);
+  if (kt < nk) iteration(StageC<1>{}, kt++);
+  if (kt < nk) iteration(StageC<2>{}, kt++);
+  // No DMA may still be writing LDS when the workgroup retires.
+  wait_vmcnt<0>();
+
+  // Epilogue.  The accumulators go through LDS so that C leaves in full
+  // 512-byte row segments (32 lanes x 16 bytes) instead of 4-byte scatters.
+  // 32x32 accumulator layout: register r of lane l holds row
+  // 8*(r/4) + 4*(l/32) + r%4, column l%32.  Each wave stages one 32-row
+  // block (32 x 128 floats) at a time in its own stage object, now idle;
+  // rows are padded to 136 floats so the two 32-lane halves of each 4-byte
+  // write land on disjoint banks.
+  __builtin_amdgcn_s_barrier();  // every wave is done reading the stages
+  constexpr int kEpRow = 136;     // floats per staged row (17 KB per wave)
+  float* ep = reinterpret_cast<float*>(wave == 0   ? dma_stage<0>()
+                                       : wave == 1 ? dma_stage<1>()
+                                       : wave == 2 ? dma_stage<2>()
+                                                   : dma_stage<3>());
+  const bool full = g.c_vec && (m0 + kTileM <= g.M) && (n0 + kTileN <= g.N);
+  const int col_l = lane & 31;
+  const int row_l = (lane >> 5) * 4;
+  const int c4 = (lane & 31) * 4;
+  const int gcol = n0 + wn * 128 + c4;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        ep[((r >> 2) * 8 + row_l + (r & 3)) * kEpRow + ni * 32 + col_l] = acc[mi][ni][r];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // Lane l stores columns 4*(l%32) .. +3 of staged rows 2*i + l/32.
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int lr = 2 * i + (lane >> 5);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(ep + lr * kEpRow + c4);
+      const int grow = m0 + wm * 128 + mi * 32 + lr;
+      float* dst = g.C + (int64_t)grow * g.ldc + gcol;
+      if (full) {
+        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst));
+      } else if (grow < g.M) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (gcol + e < g.N) dst[e] = v[e];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
 // Copy a rows x cols 16-bit matrix (row stride ld) into a zero-padded copy
 // with row stride ld_out (a multiple of 8), so the fast kernel can use
 // aligned 128-bit loads.  Columns [cols, ld_out) are written as 0.
@@ -666,10 +957,12 @@ DeviceState g_devices[kMaxDevices];
 std::once_flag g_global_once;
 int g_skinny_splits_override = 0;
 int g_tiled_sched = 1;
+int g_tiled_variant = 1;  // 0: register-staged kernel, 1: LDS-DMA ring kernel
 
 void global_init() {
   if (const char* s = getenv("HCG_SKINNY_SPLITS")) g_skinny_splits_override = atoi(s);
   if (const char* s = getenv("HCG_TILED_SCHED")) g_tiled_sched = atoi(s);
+  if (const char* s = getenv("HCG_TILED_VARIANT")) g_tiled_variant = atoi(s);
 }
 
 int current_device_state(DeviceState** out) {
@@ -755,6 +1048,14 @@ int launch_fast(const FastArgs& a, hipStream_t stream) {
   } else {
     gemm_tiled_kernel<DT, 1><<<grid, block, 0, stream>>>(a);
   }
+  HCG_HIP_CHECK(hipGetLastError());
+  return HCG_OK;
+}
+
+template <int DT>
+int launch_dma(const FastArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
+  gemm_dma_kernel<DT><<<grid, dim3(kTiledThreads), 0, stream>>>(a);
   HCG_HIP_CHECK(hipGetLastError());
   return HCG_OK;
 }
@@ -862,8 +1163,11 @@ int64_t fast_extent_b(int N, int K, int64_t ldb) {
 int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
               float* C, int64_t ldc, int M, int N, int K, hipStream_t stream, bool force_generic) {
   const int64_t kLimit = (int64_t)1 << 31;
-  const bool a_ok = aligned16(A) && lda % 8 == 0;
-  const bool b_ok = aligned16(B) && ldb % 8 == 0;
+  // The DMA kernel masks at 8-element granularity, so it also needs K and N
+  // to be multiples of 8 (or zero padding supplied by a repack).
+  const bool dma = g_tiled_variant == 1;
+  const bool a_ok = aligned16(A) && lda % 8 == 0 && (!dma || K % 8 == 0);
+  const bool b_ok = aligned16(B) && ldb % 8 == 0 && (!dma || N % 8 == 0);
   const int64_t lda_p = a_ok ? lda : (int64_t)round_up(K, 8);
   const int64_t ldb_p = b_ok ? ldb : (int64_t)round_up(N, 8);
   const int64_t tiles = (int64_t)((M + kTileM - 1) / kTileM) * ((N + kTileN - 1) / kTileN);
@@ -911,6 +1215,8 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
   // 16-byte chunk that holds it (never past that chunk).
   f.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda_p + K) * 2, 16);
   f.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * ldb_p + N) * 2, 16);
+  f.c_vec = aligned16(C) && ldc % 4 == 0;
+  if (dma) return dtype == HCG_F16 ? launch_dma<HCG_F16>(f, stream) : launch_dma<HCG_BF16>(f, stream);
   return dtype == HCG_F16 ? launch_fast<HCG_F16>(f, stream) : launch_fast<HCG_BF16>(f, stream);
 }
 
