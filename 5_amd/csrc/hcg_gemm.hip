@@ -9,12 +9,15 @@
 // 64-wide wavefronts and the v_mfma_f32_{32x32x16,16x16x32}_{f16,bf16}
 // matrix cores:
 //
-//   * gemm_tiled_kernel -- compute-bound shapes.  256x256 output tile per
+//   * gemm_dma_kernel -- compute-bound shapes.  256x256 output tile per
 //     256-thread workgroup (4 waves in 2x2, each 128x128 = 4x4 MFMA 32x32x16
-//     tiles), K step 64, double-buffered LDS, 128-bit global loads, B
-//     transposed in registers on its way to LDS so both MFMA operands read
-//     K-contiguous 128-bit fragments, XOR-swizzled LDS rows, XCD-aware tile
-//     order, masked M/N/K tails.
+//     tiles), K step 32 through a 4-stage LDS ring filled by direct
+//     global->LDS DMA loads (buffer_load ... lds), B kept row-major in LDS
+//     and read with transposing LDS loads (ds_read_b64_tr_b16), XOR-swizzled
+//     bank-conflict-free layouts, XCD-aware tile order, masked M/N/K tails
+//     by the buffer range check, and an LDS-staged 16-byte epilogue.
+//   * gemm_generic_kernel -- fallback for operands whose byte offsets do not
+//     fit 31 bits: plain pointers, register staging, any alignment.
 //   * gemm_skinny_kernel -- M <= 16 (HBM-bound).  One 16-row MFMA 16x16x32
 //     block covers all of A; B is streamed exactly once with 128-bit loads,
 //     transposed 8x8 in registers, split over K across waves and workgroups;
@@ -285,195 +288,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 
-__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-}
-
-// Mask keeping the first `valid` (clamped to [0, 8]) 16-bit lanes of a chunk.
-__device__ __forceinline__ u32x4 lane_mask(int valid) {
-  u32x4 m;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int lo = 2 * p;
-    m[p] = (valid > lo ? 0x0000ffffu : 0u) | (valid > lo + 1 ? 0xffff0000u : 0u);
-  }
-  return m;
-}
-
 // Scheduling-group masks for __builtin_amdgcn_sched_group_barrier.
 constexpr int kSgMfma = 0x008;
 constexpr int kSgVmemRead = 0x020;
 constexpr int kSgDsRead = 0x100;
-constexpr int kSgDsWrite = 0x200;
-constexpr int kSgValu = 0x002;
-
-// Interleave request for one block of 16 MFMAs: after each MFMA, up to one
-// DS read, one buffer load, one DS write and two VALU ops, while the counts
-// last (kSched == 1; kSched == 0 leaves scheduling to the compiler).
-template <int kSched, int kReads, int kVmem, int kWrites, int kValu>
-__device__ __forceinline__ void sched_hint() {
-  if constexpr (kSched == 1) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-      if constexpr (kReads > 0) if (i < kReads) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
-      if constexpr (kVmem > 0) if (i < kVmem) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 1, 0);
-      if constexpr (kWrites > 0) if (i < kWrites) __builtin_amdgcn_sched_group_barrier(kSgDsWrite, 1, 0);
-      if constexpr (kValu > 0) if (2 * i < kValu) __builtin_amdgcn_sched_group_barrier(kSgValu, 2, 0);
-    }
-  }
-}
-
-template <int DT, int kSched>
-__global__ __launch_bounds__(kTiledThreads) void gemm_tiled_kernel(FastArgs g) {
-  __shared__ u32x4 lds_a[2][kTileM * 8];
-  __shared__ u32x4 lds_b[2][kTileN * 8];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  int tm, tn;
-  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
-  const int m0 = tm * kTileM, n0 = tn * kTileN;
-  const int nk = (g.K + kTileK - 1) / kTileK;
-  const bool k_tail = (g.K % kTileK) != 0;
-
-  const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(g.A, g.a_bytes);
-  const __amdgpu_buffer_rsrc_t rsrc_b = make_rsrc(g.B, g.b_bytes);
-
-  // Staging roles.  A: thread owns 16-byte chunk a_c of rows a_r + 32 i
-  // (8 lanes read one contiguous 128-byte row segment).  B: thread owns an
-  // 8(k) x 8(n) block at rows b_kb*8 + i, columns b_n*8 .. +7 (32 lanes read
-  // 512 contiguous bytes of a row); it is transposed in registers so LDS
-  // holds B as [n][k].  Rows past M (A) or K (B) lie beyond the buffer
-  // extent and load as 0; columns past N are masked once per thread.
-  const int a_c = tid & 7, a_r = tid >> 3;
-  const int b_n = tid & 31, b_kb = tid >> 5;
-  const int a_voff = ((m0 + a_r) * g.lda + a_c * 8) * 2;
-  const int a_step_i = 32 * g.lda * 2;
-  const int b_voff = ((b_kb * 8) * g.ldb + n0 + b_n * 8) * 2;
-  const int b_step_i = g.ldb * 2;
-  const u32x4 b_colmask = lane_mask(g.N - (n0 + b_n * 8));
-
-  u32x4 ga[8], gb[8];
-
-  // Global -> registers for K tile kt.  Every offset goes into the
-  // range-checked VGPR offset (the SGPR offset is not range-checked), so no
-  // load touches memory past the extent.
-  auto load_global = [&](int kt) {
-    const int k0 = kt * kTileK;
-    const int a_base = a_voff + k0 * 2;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ga[i] = buffer_load16(rsrc_a, a_base + i * a_step_i, 0);
-    const int b_base = b_voff + k0 * g.ldb * 2;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) gb[i] = buffer_load16(rsrc_b, b_base + i * b_step_i, 0);
-  };
-
-  // Registers -> LDS for K tile kt.  A columns >= K and B rows >= K (only in
-  // a partial last tile) and B columns >= N are zeroed by select, without
-  // branches; the masks are applied here, where the data is consumed, so the
-  // loads stay in flight until then.
-  auto store_lds = [&](int kt, int buf) {
-    const int k0 = kt * kTileK;
-    const u32x4 am = lane_mask(g.K - (k0 + a_c * 8));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) lds_a[buf][swz(a_r + 32 * i, a_c)] = ga[i] & am;
-    const int kr = g.K - (k0 + b_kb * 8);
-    u32x4 bm[8], bt[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) bm[i] = (i < kr) ? (gb[i] & b_colmask) : u32x4{0, 0, 0, 0};
-    transpose8x8(bm, bt);
-#pragma unroll
-    for (int n = 0; n < 8; ++n) lds_b[buf][swz(b_n * 8 + n, b_kb)] = bt[n];
-  };
-
-  auto read_frags = [&](int buf, int kk, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
-    const int c = kk * 2 + (lane >> 5);
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) fa[mi] = lds_a[buf][swz(wm * 128 + mi * 32 + (lane & 31), c)];
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni) fb[ni] = lds_b[buf][swz(wn * 128 + ni * 32 + (lane & 31), c)];
-  };
-
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-
-  auto mfma_block = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[4]) {
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma32x32x16<DT>(fa[mi], fb[ni], acc[mi][ni]);
-  };
-
-  u32x4 fa0[4], fb0[4], fa1[4], fb1[4];
-
-  load_global(0);
-  store_lds(0, 0);
-  __syncthreads();
-  read_frags(0, 0, fa0, fb0);
-
-  // Steady state: tile kt computes from LDS buffer kt&1 while tile kt+1 is
-  // loaded (block 0), transposed and written to the other buffer (block 2).
-  // Fragments for the next 16-wide K step are read while the current 16
-  // MFMAs run.  One barrier per tile, placed so the next tile's first
-  // fragments are read under the last MFMA block.
-  for (int kt = 0; kt + 1 < nk; ++kt) {
-    const int cur = kt & 1;
-    load_global(kt + 1);
-    read_frags(cur, 1, fa1, fb1);
-    mfma_block(fa0, fb0);
-    sched_hint<kSched, 8, 16, 0, 0>();
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(cur, 2, fa0, fb0);
-    mfma_block(fa1, fb1);
-    sched_hint<kSched, 8, 0, 0, 0>();
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(cur, 3, fa1, fb1);
-    store_lds(kt + 1, cur ^ 1);
-    mfma_block(fa0, fb0);
-    sched_hint<kSched, 8, 0, 16, 24>();
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-    read_frags(cur ^ 1, 0, fa0, fb0);
-    mfma_block(fa1, fb1);
-    sched_hint<kSched, 8, 0, 0, 0>();
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  {
-    const int cur = (nk - 1) & 1;
-    read_frags(cur, 1, fa1, fb1);
-    mfma_block(fa0, fb0);
-    read_frags(cur, 2, fa0, fb0);
-    mfma_block(fa1, fb1);
-    read_frags(cur, 3, fa1, fb1);
-    mfma_block(fa0, fb0);
-    mfma_block(fa1, fb1);
-  }
-
-  // Epilogue.  32x32 accumulator layout: register r of lane l holds
-  // row 8*(r/4) + 4*(l/32) + r%4, column l%32.  Only in-bounds C is written.
-  const int col_l = lane & 31;
-  const int row_l = (lane >> 5) * 4;
-  const bool full = (m0 + kTileM <= g.M) && (n0 + kTileN <= g.N);
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
-      const int col = n0 + wn * 128 + ni * 32 + col_l;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 128 + mi * 32 + (r >> 2) * 8 + row_l + (r & 3);
-        if (full || (row < g.M && col < g.N)) g.C[(int64_t)row * g.ldc + col] = acc[mi][ni][r];
-      }
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // DMA tiled kernel: global -> LDS with buffer_load ... lds (no VGPR staging)
@@ -956,13 +774,9 @@ struct DeviceState {
 DeviceState g_devices[kMaxDevices];
 std::once_flag g_global_once;
 int g_skinny_splits_override = 0;
-int g_tiled_sched = 1;
-int g_tiled_variant = 1;  // 0: register-staged kernel, 1: LDS-DMA ring kernel
 
 void global_init() {
   if (const char* s = getenv("HCG_SKINNY_SPLITS")) g_skinny_splits_override = atoi(s);
-  if (const char* s = getenv("HCG_TILED_SCHED")) g_tiled_sched = atoi(s);
-  if (const char* s = getenv("HCG_TILED_VARIANT")) g_tiled_variant = atoi(s);
 }
 
 int current_device_state(DeviceState** out) {
@@ -1034,19 +848,6 @@ int launch_generic(const TiledArgs& a, bool vec_a, bool vec_b, hipStream_t strea
     gemm_generic_kernel<DT, false, true><<<grid, block, 0, stream>>>(a);
   } else {
     gemm_generic_kernel<DT, false, false><<<grid, block, 0, stream>>>(a);
-  }
-  HCG_HIP_CHECK(hipGetLastError());
-  return HCG_OK;
-}
-
-template <int DT>
-int launch_fast(const FastArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
-  const dim3 block(kTiledThreads);
-  if (g_tiled_sched == 0) {
-    gemm_tiled_kernel<DT, 0><<<grid, block, 0, stream>>>(a);
-  } else {
-    gemm_tiled_kernel<DT, 1><<<grid, block, 0, stream>>>(a);
   }
   HCG_HIP_CHECK(hipGetLastError());
   return HCG_OK;
@@ -1165,9 +966,8 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
   const int64_t kLimit = (int64_t)1 << 31;
   // The DMA kernel masks at 8-element granularity, so it also needs K and N
   // to be multiples of 8 (or zero padding supplied by a repack).
-  const bool dma = g_tiled_variant == 1;
-  const bool a_ok = aligned16(A) && lda % 8 == 0 && (!dma || K % 8 == 0);
-  const bool b_ok = aligned16(B) && ldb % 8 == 0 && (!dma || N % 8 == 0);
+  const bool a_ok = aligned16(A) && lda % 8 == 0 && K % 8 == 0;
+  const bool b_ok = aligned16(B) && ldb % 8 == 0 && N % 8 == 0;
   const int64_t lda_p = a_ok ? lda : (int64_t)round_up(K, 8);
   const int64_t ldb_p = b_ok ? ldb : (int64_t)round_up(N, 8);
   const int64_t tiles = (int64_t)((M + kTileM - 1) / kTileM) * ((N + kTileN - 1) / kTileN);
@@ -1216,8 +1016,7 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
   f.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda_p + K) * 2, 16);
   f.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * ldb_p + N) * 2, 16);
   f.c_vec = aligned16(C) && ldc % 4 == 0;
-  if (dma) return dtype == HCG_F16 ? launch_dma<HCG_F16>(f, stream) : launch_dma<HCG_BF16>(f, stream);
-  return dtype == HCG_F16 ? launch_fast<HCG_F16>(f, stream) : launch_fast<HCG_BF16>(f, stream);
+  return dtype == HCG_F16 ? launch_dma<HCG_F16>(f, stream) : launch_dma<HCG_BF16>(f, stream);
 }
 
 int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,

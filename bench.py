@@ -53,7 +53,24 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU time of the baseline sample")
+    p.add_argument("--profile-only", action="store_true",
+                   help="run only --steps launches of the workload's GEMM (for rocprofv3), print nothing else")
+    p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                   help="run 5 device-to-device copies of MIB MiB (calibrates FETCH_SIZE/WRITE_SIZE) and exit")
     return p.parse_args()
+
+
+def measured_traffic(kernel: str, workload: str) -> tuple[int | None, str | None]:
+    """HBM-side bytes per launch from the committed rocprofv3 summary
+    profiles/<kernel>_<workload>.md (FETCH_SIZE and WRITE_SIZE runs, each
+    scaled by a plain-copy calibration), or (None, None) if absent."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}.md")
+    if not os.path.exists(path):
+        return None, None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1]), os.path.relpath(path, ROOT)
+    return None, None
 
 
 def dtype_short(name: str) -> str:
@@ -169,7 +186,7 @@ def main() -> int:
     if args.gpus != 1:
         print(
             f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X; "
-            "the GEMM shards by N or M with no exchange (see DESIGN.md), and no multi-GPU run is part of it",
+            "the GEMM would shard by N or M with no exchange, and no multi-GPU run is part of this build",
             file=sys.stderr,
         )
         return 2
@@ -185,6 +202,25 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(device=dev)
+    if args.copy_probe:
+        n = args.copy_probe * 1024 * 1024 // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: 5 x {args.copy_probe} MiB device-to-device")
+        return 0
+    if args.profile_only:
+        a, b = make_inputs(cfg, seed=0)
+        ta, tb = to_torch(a, cfg.dtype, dev), to_torch(b, cfg.dtype, dev)
+        tc = torch.empty((cfg.m, cfg.n), dtype=torch.float32, device=dev)
+        with torch.cuda.stream(stream):
+            for _ in range(args.steps):
+                g.gemm(ta, tb, out=tc)
+        torch.cuda.synchronize()
+        log(f"profile-only: {args.steps} launches of {cfg.name}")
+        return 0
     log(f"bench: {torch.cuda.get_device_name(0)}, workload {cfg.name}")
 
     a, b = make_inputs(cfg, seed=0)
@@ -198,7 +234,7 @@ def main() -> int:
     tflops = cfg.flops / per_launch / 1e12
     log(f"bench: {cfg.name}: {per_launch * 1e6:.1f} us/launch, {tflops:.1f} TFLOP/s")
     is_skinny = cfg.m <= 16
-    kernel_name = "gemm_skinny_kernel" if is_skinny else "gemm_tiled_kernel"
+    kernel_name = "gemm_skinny_kernel" if is_skinny else "gemm_dma_kernel"
     if is_skinny:
         achieved = cfg.algorithmic_bytes / per_launch / 1e9
         roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -207,6 +243,7 @@ def main() -> int:
         roofline = {"bound": "mfma", "achieved": tflops, "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                     "frac": tflops / PEAK_F16_TFLOPS, "traffic": None}
     roofline["kernel"] = kernel_name
+    roofline["traffic"], roofline["traffic_source"] = measured_traffic(kernel_name, cfg.name)
     roofline["per_launch_us"] = per_launch * 1e6
     roofline["algorithmic_per_launch"] = cfg.algorithmic_bytes if is_skinny else cfg.flops
 

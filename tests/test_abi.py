@@ -1,0 +1,61 @@
+"""The C ABI library: it is built, loads, exports every entry point that
+include/hcg_gemm.h declares, and rejects bad arguments on the host before
+any HIP call (no GPU needed for these)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from hc.gfx950 import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hcg_gemm.h")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(hcg_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_expected_entry_points():
+    assert declared_functions() == sorted(_native.EXPORTS)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    assert os.path.exists(_native.LIB_PATH), "run 5_amd/csrc/build.py (or __graft_entry__.build())"
+    lib = _native.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.hcg_version() == 100
+
+
+@pytest.mark.parametrize(
+    "args,match",
+    [
+        ((0, 5, None, 0, None, 0, None, 0, 1, 1, 1, None), "dtype must be"),
+        ((9, 0, None, 0, None, 0, None, 0, 1, 1, 1, None), "unknown algo"),
+        ((0, 0, None, 0, None, 0, None, 0, -1, 1, 1, None), "negative extent"),
+        ((2, 0, None, 0, None, 0, None, 0, 17, 1, 1, None), "needs M <= 16"),
+        ((0, 0, None, 0, None, 0, None, 0, 2, 2, 2, None), "C is NULL"),
+        ((0, 0, 0x1000, 2, 0x1000, 2, 0x1000, 1, 2, 2, 2, None), r"ldc \(1\) < N \(2\)"),
+        ((0, 0, 0x1000, 1, 0x1000, 2, 0x1000, 2, 2, 2, 2, None), r"lda \(1\) < K \(2\)"),
+        ((0, 0, 0x1000, 2, 0x1000, 1, 0x1000, 2, 2, 2, 2, None), r"ldb \(1\) < N \(2\)"),
+        ((0, 0, None, 0, None, 0, None, 0, 1 << 31, 1, 1, None), "extent above 2\\^30"),
+    ],
+)
+def test_invalid_arguments_are_rejected_on_the_host(args, match):
+    lib = _native.load()
+    assert lib.hcg_gemm_algo(*args) == _native.HCG_EINVAL
+    assert re.search(match, _native.last_error(lib))
+
+
+def test_empty_output_is_a_noop_and_clears_the_error():
+    lib = _native.load()
+    lib.hcg_gemm_algo(0, 5, None, 0, None, 0, None, 0, 1, 1, 1, None)
+    assert _native.last_error(lib)
+    assert lib.hcg_gemm(0, None, 0, None, 0, None, 0, 0, 5, 5, None) == _native.HCG_OK
+    assert _native.last_error(lib) == ""

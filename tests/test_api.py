@@ -1,0 +1,201 @@
+"""The hc kernel-definition and launch surface (host logic, no GPU).
+
+Mirrors the reference's public-API and simulator-binding tests
+(tests/test_public_api.py:26-114, tests/test_simulator.py:170-208) for what
+the gfx950 target keeps: decorator metadata, Buffer specs, intrinsic hooks,
+symbol binding with conflict detection, geometry validation, error classes,
+and the zero-size no-op.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import hc
+import hc.gfx950 as g
+from hc import Buffer, LaunchError, SimulatorError, WorkItem, kernel, sym
+from hc._launch import prepare_launch
+from hc.simulator import SimulatorTarget
+from hc.symbols import Bindings, SymbolConflictError, ceil_div
+
+from . import _kernels
+
+
+def test_public_names_match_reference_list():
+    for name in ["Buffer", "BufferSpec", "CompiledKernel", "CurrentGroup", "IdxTypeSpec", "IndexMap",
+                 "Result", "Scope", "SubGroup", "Symbol", "TensorTypeSpec", "UndefTypeSpec",
+                 "VectorTypeSpec", "WorkGroup", "WorkItem", "as_layout", "compile", "idx_type",
+                 "index_map", "kernel", "simulator", "sym", "symbols", "tensor_type", "undef_type",
+                 "vector_type"]:
+        assert hasattr(hc, name), name
+
+
+def test_kernel_decorator_attaches_metadata_and_returns_function():
+    def f(group, x: Buffer[sym.M, np.float16]):
+        pass
+
+    out = kernel(work_shape=(sym.M,), group_shape=(64,), subgroup_size=64, literals={sym.M})(f)
+    assert out is f
+    md = f.__hc_kernel__
+    assert md.work_shape == (sym.M,) and md.group_shape == (64,) and md.subgroup_size == 64
+    assert md.literals == frozenset({sym.M})
+
+
+def test_buffer_spec_forms():
+    spec = Buffer[sym.M, sym.K, np.float16]
+    assert spec.dimensions == (sym.M, sym.K) and spec.dtype == "float16"
+    assert Buffer[sym.M].dtype is None
+    assert Buffer[sym.M, hc.bfloat16].dtype == "bfloat16"
+    assert Buffer[sym.M, np.dtype(np.float32)].dtype == "float32"
+    assert repr(Buffer[sym.M, 4, np.float32]) == "Buffer[M, 4, float32]"
+
+
+def test_intrinsic_hooks_and_fallback_detection():
+    @kernel.intrinsic(scope=WorkItem, effects="pure", const_attrs={"arch"}, result_types=hc.idx_type())
+    def with_body(x, *, arch):
+        return x + 1
+
+    @kernel.intrinsic(scope=WorkItem)
+    def bodyless(x):
+        """Doc only."""
+
+    @kernel.intrinsic(scope=WorkItem)
+    def ellipsis(x):
+        ...
+
+    assert with_body.__hc_has_fallback__ and not bodyless.__hc_has_fallback__
+    assert not ellipsis.__hc_has_fallback__
+    assert with_body.__hc_intrinsic__.const_attrs == frozenset({"arch"})
+    assert with_body.__hc_intrinsic__.result_types == (hc.idx_type(),)
+
+    @with_body.lower(target="amdgpu-gfx950")
+    def _lower(ctx, x, *, arch):
+        return None
+
+    @with_body.verify
+    def _verify(sig, target):
+        return None
+
+    assert with_body.__hc_lowerings__ == {"amdgpu-gfx950": _lower}
+    assert with_body.__hc_verify__ is _verify
+
+
+def test_gfx950_example_kernel_registers_its_intrinsic_lowering():
+    from hc.gfx950 import kernels
+
+    assert "amdgpu-gfx950" in kernels.mfma_gfx950.__hc_lowerings__
+    assert kernels.mfma_gfx950.__hc_has_fallback__
+    # Lane layout of the 32x32x16 accumulator: every (row, col) once.
+    seen = {(r, kernels.lane_column(l)) for l in range(64) for r in kernels.lane_acc_rows(l)}
+    assert seen == {(r, c) for r in range(32) for c in range(32)}
+
+
+def test_symbols_interned_eval_and_conflicts():
+    assert sym.M is sym.M
+    e = ceil_div(sym.M, 16) * 32
+    assert e.eval({sym.M: 17}) == 64 and e.eval({"M": 32}) == 64
+    b = Bindings()
+    b.bind(sym.K, 7, source="a.shape[1]")
+    b.bind(sym.K, 7, source="b.shape[0]")
+    with pytest.raises(SymbolConflictError, match="conflicting binding for K: 7 from 'b.shape\\[0\\]' vs 8"):
+        b.bind(sym.K, 8, source="b.shape[0]")
+    b.require(sym.K * 2, 14)
+    with pytest.raises(SymbolConflictError):
+        b.require(sym.K + 1, 7, source="x")
+
+
+def _arrays(m, n, k, dt=np.float16):
+    return np.zeros((m, k), dt), np.zeros((k, n), dt), np.zeros((m, n), np.float32)
+
+
+def test_prepare_launch_geometry_of_the_reference_kernel():
+    a, b, c = _arrays(100, 70, 30)
+    p = prepare_launch(_kernels.tiled_gfx11_wmma_matmul, (a, b, c), {}, g.Gfx950Target())
+    assert p.work_shape == (7 * 32, 5) and p.group_shape == (32, 1) and p.subgroup_size == 32
+    assert p.env[sym.M] == 100 and p.env[sym.N] == 70 and p.env[sym.K] == 30
+    assert p.buffer_params == ("a", "b", "c")
+
+
+@pytest.mark.parametrize(
+    "args,match",
+    [
+        (lambda: (np.zeros((4, 5), np.float32), np.zeros((5, 6), np.float16), np.zeros((4, 6), np.float32)),
+         "a dtype expected float16, got float32"),
+        (lambda: (np.zeros((4, 5), np.float16), np.zeros((6, 6), np.float16), np.zeros((4, 6), np.float32)),
+         "conflicting binding for K"),
+        (lambda: (np.zeros((4,), np.float16), np.zeros((5, 6), np.float16), np.zeros((4, 6), np.float32)),
+         "a rank does not match its Buffer annotation"),
+        (lambda: ([[1.0]], np.zeros((1, 6), np.float16), np.zeros((1, 6), np.float32)),
+         "a must be a numpy.ndarray or torch.Tensor buffer"),
+    ],
+)
+def test_launch_errors_before_execution(args, match):
+    with pytest.raises(LaunchError, match=match):
+        g.launch(_kernels.tiled_gfx11_wmma_matmul, *args(), target=g.Gfx950Target())
+
+
+def test_launch_requires_a_kernel_and_a_lowering():
+    with pytest.raises(LaunchError, match="decorated with @kernel"):
+        g.launch(lambda group: None)
+    a, b, c = _arrays(4, 4, 4)
+    with pytest.raises(LaunchError, match="no amdgpu-gfx950 lowering for kernel 'some_other_kernel'"):
+        g.launch(_kernels.some_other_kernel, a, b, c)
+    with pytest.raises(LaunchError, match="no amdgpu-gfx950 lowering"):
+        g.launch(_kernels.tiled_gfx950_mfma_matmul, np.zeros((4,), np.float16))
+
+
+def test_registered_kernel_gets_the_gemm_lowering():
+    g.register_kernel(_kernels.some_other_kernel)
+    try:
+        assert g.find_lowering(_kernels.some_other_kernel) is g.find_lowering(_kernels.tiled_gfx11_wmma_matmul)
+    finally:
+        g._LOWERINGS.pop(_kernels.some_other_kernel)
+    with pytest.raises(LaunchError, match="GEMM buffer signature"):
+        g.register_kernel(_kernels.tiled_gfx950_mfma_matmul)
+
+
+def test_zero_size_launch_is_a_noop_on_every_target():
+    a, b, c = _arrays(0, 5, 3)
+    g.launch(_kernels.tiled_gfx11_wmma_matmul, a, b, c)  # no GPU needed: nothing runs
+    hc.simulator.launch(_kernels.tiled_gfx11_wmma_matmul, a, b, c, target=SimulatorTarget())
+
+
+def test_simulator_target_validates_then_reports_no_interpreter(monkeypatch):
+    monkeypatch.delenv("HC_DEFAULT_TARGET", raising=False)
+    a, b, c = _arrays(4, 4, 4)
+    with pytest.raises(LaunchError, match="conflicting binding"):
+        hc.simulator.launch(_kernels.tiled_gfx11_wmma_matmul, a, np.zeros((5, 4), np.float16), c)
+    with pytest.raises(SimulatorError, match="host simulator is not part of this build"):
+        hc.simulator.launch(_kernels.tiled_gfx11_wmma_matmul, a, b, c)
+    with pytest.raises(LaunchError, match="group size exceeds"):
+        hc.simulator.launch(_kernels.tiled_gfx11_wmma_matmul, a, b, c, target=SimulatorTarget(max_group_size=16))
+
+
+def test_default_target_switch(monkeypatch):
+    monkeypatch.setenv("HC_DEFAULT_TARGET", "gfx950")
+    assert isinstance(hc.simulator.default_target(), g.Gfx950Target)
+    monkeypatch.setenv("HC_DEFAULT_TARGET", "")
+    assert isinstance(hc.simulator.default_target(), SimulatorTarget)
+
+
+def test_compile_handle_checks_lowering_and_pinned_symbols():
+    handle = hc.compile(_kernels.tiled_gfx11_wmma_matmul, symbols={"K": 8})
+    assert isinstance(handle, hc.CompiledKernel)
+    a, b, c = _arrays(4, 4, 7)
+    with pytest.raises(LaunchError, match="K is compiled as 8 but the arguments bind 7"):
+        handle(a, b, c)
+    with pytest.raises(LaunchError, match="no amdgpu-gfx950 lowering"):
+        hc.compile(_kernels.some_other_kernel)
+
+
+def test_gemm_entry_validates_before_touching_a_device():
+    pytest.importorskip("torch")
+    with pytest.raises(LaunchError, match="A.shape\\[1\\] must match B.shape\\[0\\]"):
+        g.gemm(np.zeros((2, 3), np.float16), np.zeros((4, 2), np.float16))
+    with pytest.raises(LaunchError, match="must both be float16 or both bfloat16"):
+        g.gemm(np.zeros((2, 3), np.float16), np.zeros((3, 2), np.float32))
+    with pytest.raises(LaunchError, match="unknown algo"):
+        g.gemm(np.zeros((2, 3), np.float16), np.zeros((3, 2), np.float16), algo="fast")
+    with pytest.raises(LaunchError, match="C shape"):
+        g.gemm(np.zeros((2, 3), np.float16), np.zeros((3, 2), np.float16), out=np.zeros((3, 3), np.float32))

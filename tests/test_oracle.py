@@ -1,0 +1,238 @@
+"""Pins for the CPU oracle (oracle/hc_oracle.py, oracle/hc_oracle.c).
+
+Each check is independent of the oracle's own formula: a scalar np.float32
+triple loop, the reference test's own blocked-sum criterion, exact integer
+arithmetic, the float64 product with the Higham error bound, library
+conversions, and planted mistakes that must be caught.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+
+import numpy as np
+import pytest
+
+import hc_oracle as oracle
+from hc.gfx950.workloads import CONFIGS, make_demo_inputs, make_inputs
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _built():
+    if not oracle.available():
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location(
+            "oracle_build", os.path.join(os.path.dirname(oracle.__file__), "build.py")
+        )
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build()
+
+
+def _rand(shape, dtype, rng, scale=1.0):
+    x = rng.uniform(-scale, scale, size=shape)
+    if dtype == oracle.F16:
+        return x.astype(np.float16)
+    return oracle.f32_to_bf16_bits(x.astype(np.float32))
+
+
+# -- conversions ------------------------------------------------------------
+
+
+def test_f16_conversion_matches_numpy_for_every_pattern():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.to_float_c(bits, oracle.F16)
+    want = bits.view(np.float16).astype(np.float32)
+    finite = np.isfinite(want)
+    assert np.array_equal(got[finite].view(np.uint32), want[finite].view(np.uint32))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(got[np.isinf(want)], want[np.isinf(want)])
+
+
+def test_bf16_rounding_matches_torch():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(11)
+    x = np.concatenate(
+        [
+            rng.normal(0, 1, 20000).astype(np.float32),
+            rng.normal(0, 0.02, 20000).astype(np.float32),
+            # exact ties: low 16 bits 0x8000, even and odd kept parts
+            (np.array([0x3F808000, 0x3F818000, 0xBF808000, 0x00008000], dtype=np.uint32)).view(np.float32),
+        ]
+    )
+    ours = oracle.f32_to_bf16_bits(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, theirs)
+
+
+def test_bf16_tie_cases_by_hand():
+    # 1 + 2^-8 is halfway between bf16 1.0 and 1 + 2^-7 -> even (1.0).
+    x = np.array([1 + 2**-8, 1 + 3 * 2**-8, -(1 + 2**-8)], dtype=np.float32)
+    assert list(oracle.f32_to_bf16_bits(x)) == [0x3F80, 0x3F82, 0xBF80]
+    assert np.array_equal(oracle.bf16_bits_to_f32(np.array([0x3F80, 0xC000], dtype=np.uint16)),
+                          np.array([1.0, -2.0], dtype=np.float32))
+
+
+# -- the sequential fold ------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [oracle.F16, oracle.BF16])
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (3, 5, 7), (8, 8, 16), (17, 19, 18), (4, 6, 33)])
+def test_sequential_equals_scalar_triple_loop(m, n, k, dtype):
+    rng = np.random.default_rng(m * 100 + n * 10 + k)
+    a, b = _rand((m, k), dtype, rng), _rand((k, n), dtype, rng)
+    seq = oracle.gemm_sequential(a, b, dtype)
+    brute = oracle.gemm_bruteforce(a, b, dtype)
+    assert np.array_equal(seq.view(np.uint32), brute.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [oracle.F16, oracle.BF16])
+@pytest.mark.parametrize("m,n,k", [(17, 19, 18), (64, 33, 100), (5, 300, 257), (130, 70, 1)])
+def test_c_oracle_bit_equal_to_numpy(m, n, k, dtype):
+    rng = np.random.default_rng(7 + m + n + k)
+    a, b = _rand((m, k), dtype, rng), _rand((k, n), dtype, rng, scale=3.0)
+    seq = oracle.gemm_sequential(a, b, dtype)
+    c = oracle.gemm_c(a, b, dtype, threads=3)
+    assert np.array_equal(seq.view(np.uint32), c.view(np.uint32))
+    rows = np.array([m - 1, 0, m // 2], dtype=np.int64)
+    cr = oracle.gemm_c_rows(a, b, rows, dtype, threads=2)
+    assert np.array_equal(cr.view(np.uint32), seq[rows].view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [oracle.F16, oracle.BF16])
+def test_integer_known_answer_is_exact(dtype):
+    # |values| <= 8 and K <= 512 keep every partial sum an integer below 2^24,
+    # so every summation order is exact: the result must equal int64 A@B.
+    rng = np.random.default_rng(5)
+    ai = rng.integers(-8, 9, size=(37, 512))
+    bi = rng.integers(-8, 9, size=(512, 29))
+    if dtype == oracle.F16:
+        a, b = ai.astype(np.float16), bi.astype(np.float16)
+    else:
+        a, b = oracle.f32_to_bf16_bits(ai.astype(np.float32)), oracle.f32_to_bf16_bits(bi.astype(np.float32))
+    want = (ai @ bi).astype(np.float32)
+    assert np.array_equal(oracle.gemm_sequential(a, b, dtype), want)
+    assert np.array_equal(oracle.gemm_c(a, b, dtype), want)
+
+
+def test_identity_and_permutation_select_rows_exactly():
+    rng = np.random.default_rng(3)
+    b = rng.uniform(-1, 1, size=(24, 40)).astype(np.float16)
+    perm = rng.permutation(24)
+    p = np.zeros((24, 24), dtype=np.float16)
+    p[np.arange(24), perm] = 1
+    assert np.array_equal(oracle.gemm_c(p, b), b[perm].astype(np.float32))
+
+
+def test_zero_k_and_empty_shapes():
+    a = np.zeros((3, 0), dtype=np.float16)
+    b = np.zeros((0, 4), dtype=np.float16)
+    assert np.array_equal(oracle.gemm_sequential(a, b), np.zeros((3, 4), np.float32))
+    assert np.array_equal(oracle.gemm_c(a, b), np.zeros((3, 4), np.float32))
+    assert oracle.gemm_c(np.zeros((0, 5), np.float16), np.zeros((5, 2), np.float16)).shape == (0, 2)
+
+
+@pytest.mark.parametrize("name,m,n,k,seed", [
+    ("ref_16x16x16_seed7", 16, 16, 16, 7),
+    ("ref_32x32x32_seed7", 32, 32, 32, 7),
+    ("ref_17x19x18_seed7", 17, 19, 18, 7),
+    ("ref_32x32x32_seed0", 32, 32, 32, 0),
+])
+def test_reference_test_shapes_within_reference_tolerance(name, m, n, k, seed):
+    # The reference's own check: simulator vs blocked fp32 sum, atol 2e-6
+    # (tests/test_examples.py:23-33; examples/amdgpu_gfx11_wmma_matmul.py:438-441).
+    a, b = make_demo_inputs(m=m, n=n, k=k, seed=seed)
+    seq = oracle.gemm_sequential(a, b)
+    np.testing.assert_allclose(seq, oracle.gemm_blocked(a, b), rtol=0.0, atol=2e-6)
+    # ... and the committed fixture holds exactly these inputs and this result.
+    fx = np.load(os.path.join(GOLDEN, f"{name}.npz"))
+    assert np.array_equal(fx["a"], a) and np.array_equal(fx["b"], b)
+    assert np.array_equal(fx["c_seq"].view(np.uint32), seq.view(np.uint32))
+
+
+def test_c1_fixture_matches_oracle():
+    fx = np.load(os.path.join(GOLDEN, "c1_128_f16_seed0.npz"))
+    a, b = make_inputs("c1_128_f16", seed=0)
+    assert np.array_equal(fx["a"], a) and np.array_equal(fx["b"], b)
+    assert np.array_equal(fx["c_seq"].view(np.uint32), oracle.gemm_c(a, b).view(np.uint32))
+
+
+def _gamma(k):
+    u = 2.0**-24
+    return k * u / (1 - k * u)
+
+
+@pytest.mark.parametrize("dtype,m,n,k", [(oracle.F16, 40, 50, 1027), (oracle.BF16, 30, 20, 4096)])
+def test_error_within_higham_bound_of_float64_product(dtype, m, n, k):
+    rng = np.random.default_rng(k)
+    a, b = _rand((m, k), dtype, rng), _rand((k, n), dtype, rng)
+    a64 = oracle.operand_to_f32(a, dtype).astype(np.float64)
+    b64 = oracle.operand_to_f32(b, dtype).astype(np.float64)
+    exact = a64 @ b64  # products exact; fp64 sum error is far below the bound
+    bound = _gamma(k) * (np.abs(a64) @ np.abs(b64))
+    got = oracle.gemm_c(a, b, dtype).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= bound)
+
+
+# -- planted mistakes must be caught --------------------------------------------
+
+
+def _dropped_last_term(a, b):
+    return oracle.gemm_sequential(a[:, :-1], b[:-1, :])
+
+
+def _sign_flipped_term(a, b):
+    c = oracle.gemm_sequential(a, b)
+    return c - 2 * np.outer(a[:, 3].astype(np.float32), b[3, :].astype(np.float32))
+
+
+def _transposed_b(a, b):
+    return oracle.gemm_sequential(a, np.ascontiguousarray(b.T))
+
+
+def _started_from_one(a, b):
+    return oracle.gemm_sequential(a, b) + np.float32(1.0)
+
+
+@pytest.mark.parametrize("mutant", [_dropped_last_term, _sign_flipped_term, _transposed_b, _started_from_one])
+def test_planted_mistakes_fail_the_checks(mutant):
+    rng = np.random.default_rng(21)
+    ai = rng.integers(-4, 5, size=(48, 48))
+    bi = rng.integers(-4, 5, size=(48, 48))
+    a, b = ai.astype(np.float16), bi.astype(np.float16)
+    want = (ai @ bi).astype(np.float32)
+    bad = mutant(a, b)
+    assert not np.array_equal(bad, want)  # integer known-answer test
+    assert not oracle.parity_check(bad, want, 48).ok  # the GPU parity criterion
+
+
+# -- the parity criterion itself -----------------------------------------------
+
+
+def test_parity_check_thresholds():
+    assert oracle.max_abs_bound(1024) == pytest.approx(2e-2)
+    assert oracle.max_abs_bound(4096) == pytest.approx(4e-2)
+    assert oracle.max_abs_bound(1027) == pytest.approx(2e-2 * math.sqrt(1027 / 1024))
+    want = np.ones((4, 4), np.float32)
+    assert oracle.parity_check(want, want, 16).ok
+    off = want.copy()
+    off[0, 0] += 0.5
+    assert not oracle.parity_check(off, want, 1024).ok  # max-abs violation
+    nan = want.copy()
+    nan[1, 1] = np.nan
+    assert not oracle.parity_check(nan, want, 1024).ok
+
+
+def test_generators_are_seeded_and_follow_the_reference_recipe():
+    a1, b1 = make_demo_inputs(m=5, n=6, k=7, seed=7)
+    rng = np.random.default_rng(7)
+    assert np.array_equal(a1, rng.uniform(-1, 1, size=(5, 7)).astype(np.float16))
+    assert np.array_equal(b1, rng.uniform(-1, 1, size=(7, 6)).astype(np.float16))
+    for name in CONFIGS:
+        x1, y1 = make_inputs(name, seed=3, m=8, n=8, k=8)
+        x2, y2 = make_inputs(name, seed=3, m=8, n=8, k=8)
+        assert np.array_equal(x1, x2) and np.array_equal(y1, y2)
