@@ -709,6 +709,272 @@ __global__ __launch_bounds__(kSkinnyThreads) void gemm_skinny_kernel(SkinnyArgs 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Streaming skinny kernel: B through LDS by DMA, split-K with an in-order
+// reduction
+// ---------------------------------------------------------------------------
+//
+// Workgroup (256 threads) = NB = 128 columns x kchunk rows of B.  B moves
+// HBM -> LDS with buffer_load ... lds in 32-row stages (8 KB, 256-byte row
+// segments, the strip width that streams best on this part), kStStages deep.
+// Wave w owns columns 32w .. 32w+31: per stage it reads its B operands with
+// transposing LDS loads (ds_read_b64_tr_b16) and issues 2 MFMA 16x16x32
+// against the 16-row A block (rows >= M read as zero).  A's 16x32 slice of
+// each stage arrives by one more DMA instruction (wave 0).
+//
+// Split-K partials go to a workspace [splits][16][N] and stream_reduce_kernel
+// sums them in order s = 0..S-1 (bit-reproducible).  A second launch is
+// cheaper here than an in-kernel last-arrival reduction: that needs either a
+// device-wide L2 write-back/invalidate per workgroup (agent-scope fences) or
+// L2-bypassing coherent loads, and both measured slower than the kernel
+// boundary.
+
+constexpr int kStN = 128;
+constexpr int kStStep = 32;
+constexpr int kStStages = 8;
+constexpr int kStBBytes = kStStep * kStN * 2;  // 8 KB
+constexpr int kStABytes = 16 * kStStep * 2;    // 1 KB
+constexpr int kStMaxSplits = 16;
+
+struct StreamArgs {
+  const uint16_t* A;
+  const uint16_t* B;
+  float* C;
+  float* ws;      // [splits][16][N] partial sums (splits > 1)
+  int lda, ldb;   // elements, multiples of 8
+  int64_t ldc;
+  int M, N, K;
+  int kchunk;     // rows per split, multiple of kStStep
+  int splits;     // 1 .. kStMaxSplits
+  int a_bytes, b_bytes;
+  bool c_vec;     // C rows 16-byte aligned at every 4th column
+};
+
+#define HCG_ST_STAGE(i)                                                             \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_stb##i[kStBBytes];   \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_sta##i[kStABytes];
+HCG_ST_STAGE(0)
+HCG_ST_STAGE(1)
+HCG_ST_STAGE(2)
+HCG_ST_STAGE(3)
+HCG_ST_STAGE(4)
+HCG_ST_STAGE(5)
+HCG_ST_STAGE(6)
+HCG_ST_STAGE(7)
+#undef HCG_ST_STAGE
+
+template <int S>
+__device__ __forceinline__ unsigned char* st_b() {
+  if constexpr (S == 0) return g_stb0;
+  else if constexpr (S == 1) return g_stb1;
+  else if constexpr (S == 2) return g_stb2;
+  else if constexpr (S == 3) return g_stb3;
+  else if constexpr (S == 4) return g_stb4;
+  else if constexpr (S == 5) return g_stb5;
+  else if constexpr (S == 6) return g_stb6;
+  else return g_stb7;
+}
+template <int S>
+__device__ __forceinline__ unsigned char* st_a() {
+  if constexpr (S == 0) return g_sta0;
+  else if constexpr (S == 1) return g_sta1;
+  else if constexpr (S == 2) return g_sta2;
+  else if constexpr (S == 3) return g_sta3;
+  else if constexpr (S == 4) return g_sta4;
+  else if constexpr (S == 5) return g_sta5;
+  else if constexpr (S == 6) return g_sta6;
+  else return g_sta7;
+}
+
+// A stage: 16 rows x 32 k (64-byte rows of 4 chunks); chunk c of row r is
+// stored at c ^ ((r >> 2) & 3), so the 16 rows read at one chunk hit 16
+// distinct 16-byte bank groups.
+__device__ __forceinline__ int sta_swz(int row, int c) { return c ^ ((row >> 2) & 3); }
+
+template <int DT>
+__global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
+  constexpr int NB = kStN;
+  constexpr int kRowBytes = NB * 2;           // bytes per staged B row
+  constexpr int kRowsPerDma = 1024 / kRowBytes;
+  constexpr int kDmaPerWave = NB / 64;        // B DMA instructions per wave per stage
+  constexpr int kColsPerWave = NB / 4;
+  constexpr int kBlocks = kColsPerWave / 16;  // MFMA column blocks per wave
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nb = blockIdx.x;
+  const int split = blockIdx.y;
+  const int n0 = nb * NB;
+  const int kbeg = split * g.kchunk;
+  const int kend = min(g.K, kbeg + g.kchunk);
+  const int nsteps = (kend - kbeg + kStStep - 1) / kStStep;
+
+  const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(g.A, g.a_bytes);
+  const __amdgpu_buffer_rsrc_t rsrc_b = make_rsrc(g.B, g.b_bytes);
+
+  // DMA roles.  B: wave w fills row blocks w*kDmaPerWave + i of the stage;
+  // lane l covers row kRowsPerDma*blk + l/(NB/8), physical chunk l%(NB/8).
+  // A (wave 0): lane l covers row l/4, physical chunk l%4.  Rows past this
+  // split's K range, rows past M and chunks past N go past the range check
+  // and load zeros.
+  int b_off[kDmaPerWave], b_row[kDmaPerWave];
+#pragma unroll
+  for (int i = 0; i < kDmaPerWave; ++i) {
+    const int blk = wave * kDmaPerWave + i;
+    const int kr = blk * kRowsPerDma + lane / (NB / 8);
+    const int cb = b_chunk_swz(kr, lane % (NB / 8));
+    b_row[i] = (n0 + cb * 8 < g.N) ? kr : 0x3fffffff;
+    b_off[i] = (kr * g.ldb + n0 + cb * 8) * 2;
+  }
+  const int a_r = lane >> 2;
+  const int a_c = sta_swz(a_r, lane & 3);
+  const bool a_ok = a_r < g.M;
+  const int a_off = (a_r * g.lda + a_c * 8) * 2;
+
+  auto issue = [&](auto sc, int step) {
+    constexpr int S = decltype(sc)::value;
+    const int k0 = kbeg + step * kStStep;
+#pragma unroll
+    for (int i = 0; i < kDmaPerWave; ++i) {
+      const int off = (k0 + b_row[i] < kend) ? b_off[i] + k0 * g.ldb * 2 : kOobOffset;
+      dma16(rsrc_b, (lds_void*)(st_b<S>() + (wave * kDmaPerWave + i) * 1024), off);
+    }
+    if (wave == 0) {
+      const int off = (a_ok && k0 + a_c * 8 < kend) ? a_off + k0 * 2 : kOobOffset;
+      dma16(rsrc_a, (lds_void*)st_a<S>(), off);
+    }
+  };
+
+  // Fragment addresses.  A operand: row l%16, k chunk l/16.  B operand for
+  // column block j of this wave, half h: source lane s = l%16 of group
+  // q = l/16 points at k row 8q + 4h + s/4, column w*NB/4 + 16j + 4(s%4).
+  const int fa = (lane & 15) * 64 + sta_swz(lane & 15, lane >> 4) * 16;
+  int fb[kBlocks][2];
+#pragma unroll
+  for (int j = 0; j < kBlocks; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int sl = lane & 15, q = lane >> 4;
+      const int krow = 8 * q + 4 * h + (sl >> 2);
+      const int ncol = wave * kColsPerWave + 16 * j + 4 * (sl & 3);
+      fb[j][h] = krow * kRowBytes + b_chunk_swz(krow, ncol >> 3) * 16 + (ncol & 7) * 2;
+    }
+
+  f32x4 acc[kBlocks];
+#pragma unroll
+  for (int j = 0; j < kBlocks; ++j) acc[j] = f32x4{};
+
+  auto compute = [&](auto sc) {
+    constexpr int S = decltype(sc)::value;
+    const u32x4 af = *reinterpret_cast<const u32x4*>(st_a<S>() + fa);
+#pragma unroll
+    for (int j = 0; j < kBlocks; ++j) {
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(st_b<S>() + fb[j][0]));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(st_b<S>() + fb[j][1]));
+      const uint64_t l64 = __builtin_bit_cast(uint64_t, lo), h64 = __builtin_bit_cast(uint64_t, hi);
+      const u32x4 bf = u32x4{(uint32_t)l64, (uint32_t)(l64 >> 32), (uint32_t)h64, (uint32_t)(h64 >> 32)};
+      acc[j] = mfma16x16x32<DT>(af, bf, acc[j]);
+    }
+  };
+
+  // One step from stage S: wait for it (this wave's DMAs; kStStages - 2
+  // newer stages may still be in flight), barrier (everyone's DMAs landed and
+  // everyone finished the stage being refilled), refill the previous stage
+  // with step + kStStages - 1, multiply.  Wave 0 has one more DMA per stage.
+  constexpr int kLater = kStStages - 2;
+  auto step_fn = [&](auto sc, int step) {
+    constexpr int S = decltype(sc)::value;
+    if (wave == 0) {
+      wait_vmcnt<(kDmaPerWave + 1) * kLater>();
+    } else {
+      wait_vmcnt<kDmaPerWave * kLater>();
+    }
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(StageC<(S + kStStages - 1) % kStStages>{}, step + kStStages - 1);
+    compute(sc);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  issue(StageC<0>{}, 0);
+  issue(StageC<1>{}, 1);
+  issue(StageC<2>{}, 2);
+  issue(StageC<3>{}, 3);
+  issue(StageC<4>{}, 4);
+  issue(StageC<5>{}, 5);
+  issue(StageC<6>{}, 6);
+
+  int step = 0;
+  for (; step + kStStages <= nsteps; step += kStStages) {
+    step_fn(StageC<0>{}, step);
+    step_fn(StageC<1>{}, step + 1);
+    step_fn(StageC<2>{}, step + 2);
+    step_fn(StageC<3>{}, step + 3);
+    step_fn(StageC<4>{}, step + 4);
+    step_fn(StageC<5>{}, step + 5);
+    step_fn(StageC<6>{}, step + 6);
+    step_fn(StageC<7>{}, step + 7);
+  }
+  if (step < nsteps) step_fn(StageC<0>{}, step++);
+  if (step < nsteps) step_fn(StageC<1>{}, step++);
+  if (step < nsteps) step_fn(StageC<2>{}, step++);
+  if (step < nsteps) step_fn(StageC<3>{}, step++);
+  if (step < nsteps) step_fn(StageC<4>{}, step++);
+  if (step < nsteps) step_fn(StageC<5>{}, step++);
+  if (step < nsteps) step_fn(StageC<6>{}, step++);
+  wait_vmcnt<0>();  // no DMA may still be writing LDS at exit
+
+  // 16x16 accumulator layout: register r of lane l holds row 4*(l/16) + r,
+  // column l%16 of the block.
+  const int ocol = n0 + wave * kColsPerWave + (lane & 15);
+  if (g.splits == 1) {
+#pragma unroll
+    for (int j = 0; j < kBlocks; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = (lane >> 4) * 4 + r, col = ocol + 16 * j;
+        if (row < g.M && col < g.N) g.C[(int64_t)row * g.ldc + col] = acc[j][r];
+      }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < kBlocks; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = (lane >> 4) * 4 + r, col = ocol + 16 * j;
+      if (col < g.N) g.ws[((int64_t)split * 16 + row) * g.N + col] = acc[j][r];
+    }
+}
+
+// C[i][j] = sum over splits s = 0..S-1 (in order) of ws[s][i][j], four
+// columns per thread (N is a multiple of 8 on this path).
+__global__ __launch_bounds__(256) void stream_reduce_kernel(const float* ws, float* C, int64_t ldc, int M,
+                                                            int N, int splits, bool c_vec) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per_row = N / 4;
+  if (idx >= (int64_t)M * per_row) return;
+  const int row = (int)(idx / per_row), col = (int)(idx % per_row) * 4;
+  f32x4 part[kStMaxSplits];
+#pragma unroll
+  for (int sp = 0; sp < kStMaxSplits; ++sp)
+    if (sp < splits) part[sp] = *reinterpret_cast<const f32x4*>(ws + ((int64_t)sp * 16 + row) * N + col);
+  f32x4 v = part[0];
+#pragma unroll
+  for (int sp = 1; sp < kStMaxSplits; ++sp)
+    if (sp < splits) v += part[sp];
+  float* dst = C + (int64_t)row * ldc + col;
+  if (c_vec) {
+    *reinterpret_cast<f32x4*>(dst) = v;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[e] = v[e];
+  }
+}
+
 // C[i][j] = sum over splits s = 0..S-1 (in order) of ws[s][i][j].
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* ws, float* C, int64_t ldc,
                                                             int M, int N, int splits) {
@@ -823,7 +1089,7 @@ int stream_workspace(DeviceState* st, hipStream_t stream, size_t bytes, void** o
   }
   if (!w->ptr) {
     void* p = nullptr;
-    const size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    const size_t want = bytes < ((size_t)2 << 20) ? ((size_t)2 << 20) : bytes;
     HCG_HIP_CHECK(hipMalloc(&p, want));
     w->ptr = p;
     w->bytes = want;
@@ -901,8 +1167,72 @@ int skinny_splits(const DeviceState* st, int N, int K) {
   return splits;
 }
 
+// Split count for the streaming kernel: about one workgroup per CU, each
+// split at least 8 stages (256 rows) long.
+int stream_splits(const DeviceState* st, int nblocks, int K) {
+  const int ksteps = (K + kStStep - 1) / kStStep;
+  int splits = g_skinny_splits_override;
+  if (splits <= 0) {
+    splits = (st->num_cus + nblocks - 1) / nblocks;
+    const int max_by_k = ksteps / 8 > 0 ? ksteps / 8 : 1;
+    if (splits > max_by_k) splits = max_by_k;
+  }
+  if (splits > ksteps) splits = ksteps;
+  if (splits > kStMaxSplits) splits = kStMaxSplits;
+  if (splits < 1) splits = 1;
+  return splits;
+}
+
+template <int DT>
+int launch_stream(const StreamArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)((a.N + kStN - 1) / kStN), (unsigned)a.splits);
+  gemm_stream_kernel<DT><<<grid, dim3(256), 0, stream>>>(a);
+  HCG_HIP_CHECK(hipGetLastError());
+  if (a.splits > 1) {
+    const int64_t total = (int64_t)a.M * (a.N / 4);
+    stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(a.ws, a.C, a.ldc, a.M, a.N,
+                                                                             a.splits, a.c_vec);
+    HCG_HIP_CHECK(hipGetLastError());
+  }
+  return HCG_OK;
+}
+
 int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
                float* C, int64_t ldc, int M, int N, int K, hipStream_t stream) {
+  const int64_t kLimit = (int64_t)1 << 31;
+  // The streaming kernel masks at 8-element granularity through the buffer
+  // range check: it needs aligned rows and K, N multiples of 8.
+  const bool stream_ok = aligned16(A) && lda % 8 == 0 && K % 8 == 0 && aligned16(B) && ldb % 8 == 0 &&
+                         N % 8 == 0 && ((int64_t)16 * lda + K) * 2 < kLimit &&
+                         ((int64_t)round_up(K, kStStep) * ldb + round_up(N, kStN)) * 2 < kLimit;
+  if (stream_ok) {
+    StreamArgs a{};
+    a.A = static_cast<const uint16_t*>(A);
+    a.B = static_cast<const uint16_t*>(B);
+    a.C = C;
+    a.lda = (int)lda;
+    a.ldb = (int)ldb;
+    a.ldc = ldc;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.splits = stream_splits(st, (N + kStN - 1) / kStN, K);
+    const int ksteps = (K + kStStep - 1) / kStStep;
+    a.kchunk = ((ksteps + a.splits - 1) / a.splits) * kStStep;
+    a.splits = (K + a.kchunk - 1) / a.kchunk;  // drop empty trailing splits
+    a.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda + K) * 2, 16);
+    a.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * ldb + N) * 2, 16);
+    a.c_vec = aligned16(C) && ldc % 4 == 0;
+    a.ws = nullptr;
+    if (a.splits > 1) {
+      void* ws = nullptr;
+      const int rc = stream_workspace(st, stream, (size_t)a.splits * 16 * (size_t)N * sizeof(float), &ws);
+      if (rc != HCG_OK) return rc;
+      a.ws = static_cast<float*>(ws);
+    }
+    return dtype == HCG_F16 ? launch_stream<HCG_F16>(a, stream) : launch_stream<HCG_BF16>(a, stream);
+  }
+  // Fallback for unaligned operands: register-staged kernel + reduce kernel.
   SkinnyArgs a{};
   a.A = static_cast<const uint16_t*>(A);
   a.B = static_cast<const uint16_t*>(B);
