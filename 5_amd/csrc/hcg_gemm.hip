@@ -297,14 +297,17 @@ constexpr int kSgDsRead = 0x100;
 // DMA tiled kernel: global -> LDS with buffer_load ... lds (no VGPR staging)
 // ---------------------------------------------------------------------------
 //
-// 256x256 output tile, 4 waves (2x2, 128x128 each, 4x4 MFMA 32x32x16), K step
-// 32, and a 4-stage LDS ring: tile kt+3 is requested while tile kt is being
-// multiplied, so each load has about three tiles of MFMA time to land.
+// TM x 256 output tile (TM = 256 or 128), 4 waves (2x2, each TM/2 x 128 =
+// TM/64 x 4 MFMA 32x32x16 tiles), K step 32, and a STAGES-deep LDS ring:
+// tile kt+STAGES-1 is requested while tile kt is multiplied.  TM = 256 uses
+// 4 stages (128 KB, one workgroup per CU); TM = 128 uses 3 stages (72 KB) so
+// two workgroups share a CU -- for shapes with too few 256x256 tiles to fill
+// the chip.
 //
-// Stage layout (32 KB): A as [256 rows][32 k] (64-byte rows of 4 chunks of
-// 16 bytes), B as [32 k][256 n] (512-byte rows of 32 chunks); chunks are
-// XOR-swizzled per row (a_chunk_swz, b_chunk_swz).  A fragments are one ds_read_b128;
-// B fragments are two ds_read_b64_tr_b16, which within each 16-lane group
+// Stage layout: A as [TM rows][32 k] (64-byte rows of 4 chunks of 16 bytes),
+// B as [32 k][256 n] (512-byte rows of 32 chunks); chunks are XOR-swizzled
+// per row (a_chunk_swz, b_chunk_swz).  A fragments are one ds_read_b128; B
+// fragments are two ds_read_b64_tr_b16, which within each 16-lane group
 // hand lane i element i%4 of source lane 4j + i/4 (j = 0..3): source lanes
 // point at 4 consecutive k rows x 16 columns, so lane i receives 4
 // consecutive k of column i, the MFMA B operand.
@@ -315,8 +318,6 @@ constexpr int kSgDsRead = 0x100;
 // range check returns zeros; rows past M (A) or K (B) are past it already.
 
 constexpr int kDmaK = 32;
-constexpr int kDmaStages = 4;
-constexpr int kDmaStageBytes = (kTileM + kTileN) * kDmaK * 2;  // 32 KB
 constexpr int kOobOffset = 0x7ffffff0;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -334,20 +335,34 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, lds_void* dst, i
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, 0, 0, 0);
 }
 
-// The four stages are separate LDS objects and every access names its stage
-// at compile time, so the compiler can tell a DMA into one stage from reads
-// of another and does not serialize them with a full vmcnt wait.
-__shared__ __attribute__((aligned(1024))) unsigned char g_stage0[kDmaStageBytes];
-__shared__ __attribute__((aligned(1024))) unsigned char g_stage1[kDmaStageBytes];
-__shared__ __attribute__((aligned(1024))) unsigned char g_stage2[kDmaStageBytes];
-__shared__ __attribute__((aligned(1024))) unsigned char g_stage3[kDmaStageBytes];
+template <int TM>
+constexpr int dma_stage_bytes() {
+  return (TM + kTileN) * kDmaK * 2;
+}
 
-template <int S>
+// Each stage is a separate LDS object and every access names its stage at
+// compile time, so the compiler can tell a DMA into one stage from reads of
+// another and does not serialize them with a full vmcnt wait.
+__shared__ __attribute__((aligned(1024))) unsigned char g_t256_s0[dma_stage_bytes<256>()];
+__shared__ __attribute__((aligned(1024))) unsigned char g_t256_s1[dma_stage_bytes<256>()];
+__shared__ __attribute__((aligned(1024))) unsigned char g_t256_s2[dma_stage_bytes<256>()];
+__shared__ __attribute__((aligned(1024))) unsigned char g_t256_s3[dma_stage_bytes<256>()];
+__shared__ __attribute__((aligned(1024))) unsigned char g_t128_s0[dma_stage_bytes<128>()];
+__shared__ __attribute__((aligned(1024))) unsigned char g_t128_s1[dma_stage_bytes<128>()];
+__shared__ __attribute__((aligned(1024))) unsigned char g_t128_s2[dma_stage_bytes<128>()];
+
+template <int TM, int S>
 __device__ __forceinline__ unsigned char* dma_stage() {
-  if constexpr (S == 0) return g_stage0;
-  else if constexpr (S == 1) return g_stage1;
-  else if constexpr (S == 2) return g_stage2;
-  else return g_stage3;
+  if constexpr (TM == 256) {
+    if constexpr (S == 0) return g_t256_s0;
+    else if constexpr (S == 1) return g_t256_s1;
+    else if constexpr (S == 2) return g_t256_s2;
+    else return g_t256_s3;
+  } else {
+    if constexpr (S == 0) return g_t128_s0;
+    else if constexpr (S == 1) return g_t128_s1;
+    else return g_t128_s2;
+  }
 }
 
 template <int S>
@@ -360,17 +375,23 @@ __device__ __forceinline__ int a_chunk_swz(int row, int c) {
   return c ^ ((row >> 1) & 3) ^ ((row >> 3) & 1);
 }
 
-// Physical chunk of logical chunk c in B row k (32 chunks/row).  A 32-lane
-// transposed read touches 4 consecutive k rows x 4 consecutive chunks; the
-// XOR pattern {0, 4, 10, 14} makes those 16 accesses distinct modulo 16
-// (64 banks) and each 16-lane half distinct modulo 8 (32 banks).
+// Physical chunk of logical chunk c in B row k (16 or 32 chunks/row).  A
+// 32-lane transposed read touches 4 consecutive k rows x 4 consecutive
+// chunks; the XOR pattern {0, 4, 10, 14} makes those 16 accesses distinct
+// modulo 16 (64 banks) and each 16-lane half distinct modulo 8 (32 banks).
 __device__ __forceinline__ int b_chunk_swz(int k, int c) {
   const int m = k & 3;
   return c ^ ((m >> 1) * 10 + (m & 1) * 4);
 }
 
-template <int DT>
-__global__ __launch_bounds__(kTiledThreads) void gemm_dma_kernel(FastArgs g) {
+template <int DT, int TM, int STAGES>
+__global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_kernel(FastArgs g) {
+  static_assert((TM == 256 && STAGES == 4) || (TM == 128 && STAGES == 3), "tile variant");
+  constexpr int kMi = TM / 64;            // 32-row MFMA tiles per wave
+  constexpr int kADma = TM / 64;          // A DMA instructions per wave per stage
+  constexpr int kDmaPerWave = kADma + 4;  // + 4 for B
+  constexpr int kABytes = TM * kDmaK * 2;
+
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   // Wave index as a provably uniform value: it feeds the LDS base (M0) of
@@ -380,26 +401,30 @@ __global__ __launch_bounds__(kTiledThreads) void gemm_dma_kernel(FastArgs g) {
 
   int tm, tn;
   tile_coords(g.tiles_m, g.tiles_n, tm, tn);
-  const int m0 = tm * kTileM, n0 = tn * kTileN;
+  const int m0 = tm * TM, n0 = tn * kTileN;
   const int nk = (g.K + kDmaK - 1) / kDmaK;
 
   const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(g.A, g.a_bytes);
   const __amdgpu_buffer_rsrc_t rsrc_b = make_rsrc(g.B, g.b_bytes);
 
   // DMA roles.  Each wave instruction fills 1 KB of LDS, lane l at byte
-  // 16*l.  A: wave w owns 16-row blocks 4w..4w+3; lane l covers row
-  // blk*16 + l/4 at physical chunk l%4, so it loads the logical chunk that
-  // the swizzle puts there (the swizzles are XOR involutions).  B: wave w
-  // owns 2-row blocks 4w..4w+3; lane l covers k row blk*2 + l/32 at
+  // 16*l.  A: wave w owns 16-row blocks kADma*w .. +kADma-1; lane l covers
+  // row blk*16 + l/4 at physical chunk l%4, so it loads the logical chunk
+  // that the swizzle puts there (the swizzles are XOR involutions).  B: wave
+  // w owns 2-row blocks 4w..4w+3; lane l covers k row blk*2 + l/32 at
   // physical chunk l%32.
-  int a_off[4], a_col[4], b_off[4], b_row[4];
+  int a_off[kADma], a_col[kADma], b_off[4], b_row[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int blk = wave * 4 + i;
+  for (int i = 0; i < kADma; ++i) {
+    const int blk = wave * kADma + i;
     const int row = blk * 16 + (lane >> 2);
     const int c = a_chunk_swz(row, lane & 3);
     a_col[i] = c * 8;
     a_off[i] = ((m0 + row) * g.lda + c * 8) * 2;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int blk = wave * 4 + i;
     const int kr = blk * 2 + (lane >> 5);
     const int cb = b_chunk_swz(kr, lane & 31);
     // Columns past N never change with k: push such a chunk's row out of
@@ -409,27 +434,27 @@ __global__ __launch_bounds__(kTiledThreads) void gemm_dma_kernel(FastArgs g) {
   }
 
   auto issue_tile = [&](auto sc, int kt) {
-    unsigned char* st = dma_stage<decltype(sc)::value>();
+    unsigned char* st = dma_stage<TM, decltype(sc)::value>();
     const int k0 = kt * kDmaK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kADma; ++i) {
       const int off = (k0 + a_col[i] < g.K) ? a_off[i] + k0 * 2 : kOobOffset;
-      dma16(rsrc_a, (lds_void*)(st + (wave * 4 + i) * 1024), off);
+      dma16(rsrc_a, (lds_void*)(st + (wave * kADma + i) * 1024), off);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int off = (k0 + b_row[i] < g.K) ? b_off[i] + k0 * g.ldb * 2 : kOobOffset;
-      dma16(rsrc_b, (lds_void*)(st + kTileM * kDmaK * 2 + (wave * 4 + i) * 1024), off);
+      dma16(rsrc_b, (lds_void*)(st + kABytes + (wave * 4 + i) * 1024), off);
     }
   };
 
   // Fragment addresses (bytes within a stage).
-  int fa_addr[2][4], fb_addr[2][4][2];
+  int fa_addr[2][kMi], fb_addr[2][4][2];
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      const int row = wm * 128 + mi * 32 + (lane & 31);
+    for (int mi = 0; mi < kMi; ++mi) {
+      const int row = wm * (TM / 2) + mi * 32 + (lane & 31);
       const int c = kk * 2 + (lane >> 5);
       fa_addr[kk][mi] = row * 64 + a_chunk_swz(row, c) * 16;
     }
@@ -440,16 +465,15 @@ __global__ __launch_bounds__(kTiledThreads) void gemm_dma_kernel(FastArgs g) {
         const int sl = lane & 15, grp = lane >> 4;
         const int krow = kk * 16 + 8 * (grp >> 1) + 4 * h + (sl >> 2);
         const int ncol = wn * 128 + ni * 32 + 16 * (grp & 1) + 4 * (sl & 3);
-        const int c = ncol >> 3;
-        fb_addr[kk][ni][h] = kTileM * kDmaK * 2 + krow * 512 + b_chunk_swz(krow, c) * 16 + (ncol & 7) * 2;
+        fb_addr[kk][ni][h] = kABytes + krow * 512 + b_chunk_swz(krow, ncol >> 3) * 16 + (ncol & 7) * 2;
       }
     }
   }
 
-  auto read_frags = [&](auto sc, int kk, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
-    const unsigned char* st = dma_stage<decltype(sc)::value>();
+  auto read_frags = [&](auto sc, int kk, u32x4 (&fa)[kMi], u32x4 (&fb)[4]) {
+    const unsigned char* st = dma_stage<TM, decltype(sc)::value>();
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) fa[mi] = *reinterpret_cast<const u32x4*>(st + fa_addr[kk][mi]);
+    for (int mi = 0; mi < kMi; ++mi) fa[mi] = *reinterpret_cast<const u32x4*>(st + fa_addr[kk][mi]);
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) {
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -461,20 +485,21 @@ __global__ __launch_bounds__(kTiledThreads) void gemm_dma_kernel(FastArgs g) {
     }
   };
 
-  f32x16 acc[4][4];
+  f32x16 acc[kMi][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kMi; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  auto mfma_block = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[4]) {
+  auto mfma_block = [&](const u32x4 (&fa)[kMi], const u32x4 (&fb)[4]) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < kMi; ++mi)
 #pragma unroll
       for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma32x32x16<DT>(fa[mi], fb[ni], acc[mi][ni]);
   };
 
-  u32x4 fa0[4], fb0[4], fa1[4], fb1[4];
+  constexpr int kReads = kMi + 8;  // LDS reads per 16-wide K step
+  u32x4 fa0[kMi], fb0[4], fa1[kMi], fb1[4];
 
   // One K tile from stage S.  On entry fa0/fb0 hold its first 16-wide K
   // step; on exit they hold the next tile's.
@@ -482,126 +507,168 @@ __global__ __launch_bounds__(kTiledThreads) void gemm_dma_kernel(FastArgs g) {
     constexpr int S = decltype(sc)::value;
     read_frags(sc, 1, fa1, fb1);
     mfma_block(fa0, fb0);
-    // Issue the 12 fragment reads early, between the first MFMAs.
+    // Issue the fragment reads early, between the first MFMAs.
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
+    for (int i = 0; i < kReads / 2; ++i) {
       __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSgMfma, 10, 0);
+    __builtin_amdgcn_sched_group_barrier(kSgMfma, 4 * kMi - kReads / 2, 0);
     __builtin_amdgcn_sched_barrier(0);
-    // Tile kt+1 has landed for this wave (tile kt+2 may still be in flight);
-    // this wave's fragment reads of tile kt are complete.
-    wait_vmcnt<8>();
+    // Tile kt+1 has landed for this wave (later tiles may still be in
+    // flight); this wave's fragment reads of tile kt are complete.
+    wait_vmcnt<(STAGES - 3) * kDmaPerWave>();
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    // Every wave is past its reads of tile kt-1: its stage takes tile kt+3
-    // (tiles past K load zeros and are never multiplied).
-    issue_tile(StageC<(S + 3) & 3>{}, kt + 3);
-    read_frags(StageC<(S + 1) & 3>{}, 0, fa0, fb0);
+    // Every wave is past its reads of tile kt-1: its stage takes tile
+    // kt+STAGES-1 (tiles past K load zeros and are never multiplied).
+    issue_tile(StageC<(S + STAGES - 1) % STAGES>{}, kt + STAGES - 1);
+    read_frags(StageC<(S + 1) % STAGES>{}, 0, fa0, fb0);
     mfma_block(fa1, fb1);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < kDmaPerWave; ++i) {
       __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 1, 0);
-      if (i < 6) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+      if (2 * i < kReads) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSgMfma, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(kSgMfma, 4 * kMi - kDmaPerWave, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Prologue: tiles 0..2 in flight.
+  // Prologue: tiles 0..STAGES-2 in flight; wait for tile 0.
   issue_tile(StageC<0>{}, 0);
   issue_tile(StageC<1>{}, 1);
-  issue_tile(StageC<2>{}, 2);
-  wait_vmcnt<16>();
+  if constexpr (STAGES == 4) issue_tile(StageC<2>{}, 2);
+  wait_vmcnt<(STAGES - 2) * kDmaPerWave>();
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   read_frags(StageC<0>{}, 0, fa0, fb0);
 
   int kt = 0;
-  for (; kt + 4 <= nk; kt += 4) {
+  for (; kt + STAGES <= nk; kt += STAGES) {
     iteration(StageC<0>{}, kt);
     iteration(StageC<1>{}, kt + 1);
     iteration(StageC<2>{}, kt + 2);
-    iteration(StageC<3>{}, kt + 3);
+    if constexpr (STAGES == 4) iteration(StageC<3 % STAGES>{}, kt + 3);
   }
   if (kt < nk) iteration(StageC<0>{}, kt++);
   if (kt < nk) iteration(StageC<1>{}, kt++);
-  if (kt < nk) iteration(StageC<2>{}, kt++);
+  if constexpr (STAGES == 4)
+    if (kt < nk) iteration(StageC<2>{}, kt++);
   // No DMA may still be writing LDS when the workgroup retires.
   wait_vmcnt<0>();
 
   // Epilogue.  The accumulators go through LDS so that C leaves in full
   // 512-byte row segments (32 lanes x 16 bytes) instead of 4-byte scatters.
   // 32x32 accumulator layout: register r of lane l holds row
-  // 8*(r/4) + 4*(l/32) + r%4, column l%32.  Each wave stages one 32-row
-  // block (32 x 128 floats) at a time in its own stage object, now idle;
-  // rows are padded to 136 floats so the two 32-lane halves of each 4-byte
-  // write land on disjoint banks.
+  // 8*(r/4) + 4*(l/32) + r%4, column l%32, so registers 0-7 cover rows 0-15
+  // and 8-15 rows 16-31.  Each wave stages 16 rows x 128 columns at a time in
+  // its own 8.5 KB slice of the (now idle) stage memory; rows are padded to
+  // 136 floats so the two 32-lane halves of each 4-byte write land on
+  // disjoint banks.
   __builtin_amdgcn_s_barrier();  // every wave is done reading the stages
-  constexpr int kEpRow = 136;     // floats per staged row (17 KB per wave)
-  float* ep = reinterpret_cast<float*>(wave == 0   ? dma_stage<0>()
-                                       : wave == 1 ? dma_stage<1>()
-                                       : wave == 2 ? dma_stage<2>()
-                                                   : dma_stage<3>());
-  const bool full = g.c_vec && (m0 + kTileM <= g.M) && (n0 + kTileN <= g.N);
+  constexpr int kEpRow = 136;     // floats per staged row
+  float* ep = reinterpret_cast<float*>((wave < 2 ? dma_stage<TM, 0>() : dma_stage<TM, 1>()) +
+                                       (wave & 1) * (16 * kEpRow * 4));
+  const bool full = g.c_vec && (m0 + TM <= g.M) && (n0 + kTileN <= g.N);
   const int col_l = lane & 31;
   const int row_l = (lane >> 5) * 4;
   const int c4 = (lane & 31) * 4;
   const int gcol = n0 + wn * 128 + c4;
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
+  for (int mi = 0; mi < kMi; ++mi) {
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni)
+    for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        ep[((r >> 2) * 8 + row_l + (r & 3)) * kEpRow + ni * 32 + col_l] = acc[mi][ni][r];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // Lane l stores columns 4*(l%32) .. +3 of staged rows 2*i + l/32.
+      for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int lr = 2 * i + (lane >> 5);
-      const f32x4 v = *reinterpret_cast<const f32x4*>(ep + lr * kEpRow + c4);
-      const int grow = m0 + wm * 128 + mi * 32 + lr;
-      float* dst = g.C + (int64_t)grow * g.ldc + gcol;
-      if (full) {
-        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst));
-      } else if (grow < g.M) {
+        for (int r = 8 * hh; r < 8 * hh + 8; ++r)
+          ep[(((r >> 2) & 1) * 8 + row_l + (r & 3)) * kEpRow + ni * 32 + col_l] = acc[mi][ni][r];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // Lane l stores columns 4*(l%32) .. +3 of staged rows 2*i + l/32.
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (gcol + e < g.N) dst[e] = v[e];
+      for (int i = 0; i < 8; ++i) {
+        const int lr = 2 * i + (lane >> 5);
+        const f32x4 v = *reinterpret_cast<const f32x4*>(ep + lr * kEpRow + c4);
+        const int grow = m0 + wm * (TM / 2) + mi * 32 + hh * 16 + lr;
+        float* dst = g.C + (int64_t)grow * g.ldc + gcol;
+        if (full) {
+          __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst));
+        } else if (grow < g.M) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (gcol + e < g.N) dst[e] = v[e];
+        }
       }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 }
 
-// Copy a rows x cols 16-bit matrix (row stride ld) into a zero-padded copy
-// with row stride ld_out (a multiple of 8), so the fast kernel can use
-// aligned 128-bit loads.  Columns [cols, ld_out) are written as 0.
-__global__ __launch_bounds__(256) void repack_kernel(const uint16_t* src, int64_t ld, int rows, int cols,
-                                                     uint16_t* dst, int ld_out) {
-  const int64_t chunks_per_row = ld_out / 8;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)rows * chunks_per_row) return;
-  const int row = (int)(idx / chunks_per_row);
-  const int c0 = (int)(idx % chunks_per_row) * 8;
-  const uint16_t* p = src + (int64_t)row * ld;
+// Copies of up to two rows x cols 16-bit matrices (row stride ld) into
+// zero-padded copies with row stride ld_out (a multiple of 8), so the DMA
+// kernels can use aligned 128-bit loads.  Columns [cols, ld_out) become 0.
+struct RepackJob {
+  const uint16_t* src;
+  int64_t ld;
+  int rows, cols;
+  uint16_t* dst;
+  int ld_out;
+  int64_t chunks;  // rows * ld_out / 8
+};
+
+// One 8-element output chunk.  A chunk that lies inside the row is read as
+// aligned 4-byte words: 4 words when its first element starts a word, else 5
+// words and a 16-bit funnel shift.  The first and last words read each hold
+// an element of the chunk, so no read leaves the words that hold valid
+// data.  The row's final, partial chunk is read element by element.
+__device__ __forceinline__ void repack_chunk(const RepackJob& j, int64_t idx) {
+  const int64_t per_row = j.ld_out / 8;
+  const int row = (int)(idx / per_row);
+  const int c0 = (int)(idx % per_row) * 8;
+  const int64_t f = (int64_t)row * j.ld + c0;  // flat source element index
   uint32_t w[4];
+  if (c0 + 8 <= j.cols) {
+    // Element index counted from the 4-byte boundary at or below src.
+    const int off = (int)((reinterpret_cast<uintptr_t>(j.src) >> 1) & 1);
+    const int64_t g = f + off;
+    const uint32_t* q =
+        reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(j.src) - 2 * off) + (g >> 1);
+    if ((g & 1) == 0) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int c = c0 + 2 * q;
-    const uint32_t lo = c < cols ? p[c] : 0u;
-    const uint32_t hi = c + 1 < cols ? p[c + 1] : 0u;
-    w[q] = lo | (hi << 16);
+      for (int i = 0; i < 4; ++i) w[i] = q[i];
+    } else {
+      uint32_t v[5];
+#pragma unroll
+      for (int i = 0; i < 5; ++i) v[i] = q[i];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = (v[i] >> 16) | (v[i + 1] << 16);
+    }
+  } else {
+    const uint16_t* p = j.src + f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = c0 + 2 * i;
+      const uint32_t lo = c < j.cols ? p[2 * i] : 0u;
+      const uint32_t hi = c + 1 < j.cols ? p[2 * i + 1] : 0u;
+      w[i] = lo | (hi << 16);
+    }
   }
-  *reinterpret_cast<u32x4*>(dst + (int64_t)row * ld_out + c0) = u32x4{w[0], w[1], w[2], w[3]};
+  *reinterpret_cast<u32x4*>(j.dst + (int64_t)row * j.ld_out + c0) = u32x4{w[0], w[1], w[2], w[3]};
+}
+
+__global__ __launch_bounds__(256) void repack_kernel(RepackJob a, RepackJob b) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx < a.chunks) {
+    repack_chunk(a, idx);
+  } else if (idx - a.chunks < b.chunks) {
+    repack_chunk(b, idx - a.chunks);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1120,9 +1187,13 @@ int launch_generic(const TiledArgs& a, bool vec_a, bool vec_b, hipStream_t strea
 }
 
 template <int DT>
-int launch_dma(const FastArgs& a, hipStream_t stream) {
+int launch_dma(const FastArgs& a, int tile_m, hipStream_t stream) {
   const dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
-  gemm_dma_kernel<DT><<<grid, dim3(kTiledThreads), 0, stream>>>(a);
+  if (tile_m == 256) {
+    gemm_dma_kernel<DT, 256, 4><<<grid, dim3(kTiledThreads), 0, stream>>>(a);
+  } else {
+    gemm_dma_kernel<DT, 128, 3><<<grid, dim3(kTiledThreads), 0, stream>>>(a);
+  }
   HCG_HIP_CHECK(hipGetLastError());
   return HCG_OK;
 }
@@ -1316,18 +1387,18 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
     if (rc != HCG_OK) return rc;
     uint16_t* a_p = static_cast<uint16_t*>(ws);
     uint16_t* b_p = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + a_sz);
+    RepackJob ja{}, jb{};
     if (!a_ok) {
-      const int64_t n = (int64_t)M * (lda_p / 8);
-      repack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(a_use, lda, M, K, a_p, (int)lda_p);
-      HCG_HIP_CHECK(hipGetLastError());
+      ja = RepackJob{a_use, lda, M, K, a_p, (int)lda_p, (int64_t)M * (lda_p / 8)};
       a_use = a_p;
     }
     if (!b_ok) {
-      const int64_t n = (int64_t)K * (ldb_p / 8);
-      repack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(b_use, ldb, K, N, b_p, (int)ldb_p);
-      HCG_HIP_CHECK(hipGetLastError());
+      jb = RepackJob{b_use, ldb, K, N, b_p, (int)ldb_p, (int64_t)K * (ldb_p / 8)};
       b_use = b_p;
     }
+    const int64_t n = ja.chunks + jb.chunks;
+    repack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(ja, jb);
+    HCG_HIP_CHECK(hipGetLastError());
   }
   FastArgs f{};
   f.A = a_use;
@@ -1339,14 +1410,18 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
   f.M = M;
   f.N = N;
   f.K = K;
-  f.tiles_m = (M + kTileM - 1) / kTileM;
+  // 256-row tiles when they fill the chip (one workgroup per CU); otherwise
+  // 128-row tiles, two workgroups per CU.
+  const int64_t tiles256 = (int64_t)((M + 255) / 256) * ((N + kTileN - 1) / kTileN);
+  const int tile_m = tiles256 >= st->num_cus ? 256 : 128;
+  f.tiles_m = (M + tile_m - 1) / tile_m;
   f.tiles_n = (N + kTileN - 1) / kTileN;
   // Range-check extents cover the last valid element, rounded up to the
   // 16-byte chunk that holds it (never past that chunk).
   f.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda_p + K) * 2, 16);
   f.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * ldb_p + N) * 2, 16);
   f.c_vec = aligned16(C) && ldc % 4 == 0;
-  return dtype == HCG_F16 ? launch_dma<HCG_F16>(f, stream) : launch_dma<HCG_BF16>(f, stream);
+  return dtype == HCG_F16 ? launch_dma<HCG_F16>(f, tile_m, stream) : launch_dma<HCG_BF16>(f, tile_m, stream);
 }
 
 int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,

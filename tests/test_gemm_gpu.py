@@ -146,6 +146,27 @@ def test_tails_f16(m, n, k, algo):
     _check(_gemm(a, b, algo), oracle.gemm_c(a, b), k)
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("m,n,k", [(4095, 4100, 1000), (4096, 4096, 520), (4352, 3840, 96)])
+def test_large_tile_variant_tails(m, n, k, dtype):
+    """Shapes with at least 256 tiles of 256x256 take the 256-row tile
+    variant; ragged M, N and K tails on it."""
+    from hc.gfx950.workloads import make_inputs
+
+    print(f"case large-tile {dtype} m={m} n={n} k={k}", flush=True)
+    cfg = "c2_4096_f16" if dtype == "float16" else "c3_8192_bf16"
+    a, b = make_inputs(cfg, seed=m + k, m=m, n=n, k=k)
+    _check(_gemm(a, b, dtype=dtype), oracle.gemm_c(a, b, _dt(dtype)), k)
+
+
+def test_large_tile_variant_integer_bit_exact():
+    rng = np.random.default_rng(8)
+    ai = rng.integers(-4, 5, size=(4096, 512))
+    bi = rng.integers(-4, 5, size=(512, 4104))
+    got = _gemm(ai.astype(np.float16), bi.astype(np.float16))
+    assert np.array_equal(got, (ai @ bi).astype(np.float32))
+
+
 @pytest.mark.parametrize("m,n,k", [(17, 19, 18), (300, 520, 200), (1000, 1000, 1000), (2048, 512, 3000)])
 def test_tails_bf16(m, n, k):
     from hc.gfx950.workloads import make_inputs
