@@ -240,7 +240,7 @@ def main() -> int:
     tflops = cfg.flops / per_launch / 1e12
     log(f"bench: {cfg.name}: {per_launch * 1e6:.1f} us/launch, {tflops:.1f} TFLOP/s")
     is_skinny = cfg.m <= 16
-    kernel_name = "gemm_skinny_kernel" if is_skinny else "gemm_dma_kernel"
+    kernel_name = "gemm_stream_kernel" if is_skinny else "gemm_dma_kernel"
     if is_skinny:
         achieved = cfg.algorithmic_bytes / per_launch / 1e9
         roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
