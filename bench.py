@@ -128,6 +128,32 @@ def cpu_baseline(cfg, a, b, target_s: float) -> dict:
         "kind": "port",
         "sample": f"rows 0..{rows - 1} of {cfg.name} ({rows}x{cfg.n}x{cfg.k}), {elapsed:.1f} s, "
         f"C oracle (sequential fp32 fold, OpenMP over row blocks) on {os.cpu_count()} host CPUs",
+        "simulator_shape": simulator_shape_baseline(cfg),
+    }
+
+
+def simulator_shape_baseline(cfg) -> dict:
+    """The reference's own CPU path shape: per-lane NumPy scalar MACs.
+
+    Times hc_oracle.simulate_lane_structure (one Python-level float32 MAC per
+    lane, row and k, workgroup by workgroup, as hc.simulator executes the
+    kernel's fallback bodies) on the 128^3 configuration, on one core, and
+    projects that rate linearly to the headline workload.
+    """
+    import hc_oracle
+    from hc.gfx950.workloads import make_inputs
+
+    a, b = make_inputs("c1_128_f16", seed=0)
+    t0 = time.perf_counter()
+    hc_oracle.simulate_lane_structure(a, b)
+    elapsed = time.perf_counter() - t0
+    rate = 2.0 * 128**3 / elapsed
+    return {
+        "value": rate / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "sample": f"c1_128_f16 (128x128x128) in {elapsed:.2f} s, Python per-lane float32 MACs",
+        "projected_headline_s": 2.0 * cfg.m * cfg.n * cfg.k / rate,
     }
 
 

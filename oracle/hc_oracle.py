@@ -29,6 +29,8 @@ Parity pins for each function live in tests/test_oracle.py:
   hand-computed tie cases.
 * :func:`parity_check` -- its tolerance arithmetic is checked on planted
   errors (a dropped k term, a transposed operand) that must fail.
+* :func:`simulate_lane_structure` -- bit-exact against the scalar triple loop
+  (used only to time the reference's CPU path shape).
 """
 
 from __future__ import annotations
@@ -135,6 +137,54 @@ def gemm_blocked(a: np.ndarray, b: np.ndarray, dtype: int = F16, block: int = 16
     for k0 in range(0, a32.shape[1], block):
         out += a32[:, k0 : k0 + block] @ b32[k0 : k0 + block, :]
     return out
+
+
+def simulate_lane_structure(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """The reference simulator's work structure, for timing its CPU path.
+
+    Walks the launch the way hc.simulator runs tiled_gfx11_wmma_matmul:
+    one workgroup per 16x16 C tile in dim-0-fastest order
+    (hc/simulator.py:917-931, 1298-1301), a K loop in 16-wide steps
+    (examples/amdgpu_gfx11_wmma_matmul.py:315-324) over masked 16x16 tile
+    copies (hc/simulator.py:1338-1357), and per step the wave32 lanes'
+    fallback MACs: lane l owns column l % 16 and rows l//16, l//16 + 2, ...
+    (examples/amdgpu_gfx11_wmma_matmul.py:86-93, 177-190), each an
+    np.float32 scalar multiply-add.  Greenlet switching, masks and the
+    profile hook are not modelled, so this understates the simulator's
+    cost.  fp16 only; small shapes only (one Python MAC per flop pair).
+    """
+    m, k = a.shape
+    _, n = b.shape
+    c = np.zeros((m, n), dtype=np.float32)
+    a32 = a.astype(np.float32)
+    b32 = b.astype(np.float32)
+    for gj in range((n + 15) // 16):
+        for gi in range((m + 15) // 16):
+            r0, c0 = gi * 16, gj * 16
+            acc = [[np.float32(0.0)] * 8 for _ in range(32)]
+            for k0 in range(0, k, 16):
+                at = np.zeros((16, 16), dtype=np.float32)
+                bt = np.zeros((16, 16), dtype=np.float32)
+                blk_a = a32[r0 : r0 + 16, k0 : k0 + 16]
+                blk_b = b32[k0 : k0 + 16, c0 : c0 + 16]
+                at[: blk_a.shape[0], : blk_a.shape[1]] = blk_a
+                bt[: blk_b.shape[0], : blk_b.shape[1]] = blk_b
+                for lane in range(32):
+                    col = lane % 16
+                    frag = acc[lane]
+                    for idx, row in enumerate(range(lane // 16, 16, 2)):
+                        s = frag[idx]
+                        for kk in range(16):
+                            s += at[row, kk] * bt[kk, col]
+                        frag[idx] = s
+            for lane in range(32):
+                col = c0 + lane % 16
+                if col >= n:
+                    continue
+                for idx, row in enumerate(range(lane // 16, 16, 2)):
+                    if r0 + row < m:
+                        c[r0 + row, col] = acc[lane][idx]
+    return c
 
 
 # --------------------------------------------------------------------------

@@ -236,3 +236,10 @@ def test_generators_are_seeded_and_follow_the_reference_recipe():
         x1, y1 = make_inputs(name, seed=3, m=8, n=8, k=8)
         x2, y2 = make_inputs(name, seed=3, m=8, n=8, k=8)
         assert np.array_equal(x1, x2) and np.array_equal(y1, y2)
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 16, 16), (17, 19, 18), (33, 20, 40)])
+def test_lane_structured_simulation_is_the_same_fold(m, n, k):
+    a, b = make_demo_inputs(m=m, n=n, k=k, seed=5)
+    got = oracle.simulate_lane_structure(a, b)
+    assert np.array_equal(got.view(np.uint32), oracle.gemm_bruteforce(a, b).view(np.uint32))
