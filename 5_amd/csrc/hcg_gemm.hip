@@ -331,8 +331,8 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, lds_void* dst, int voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, 0, 0, 0);
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, lds_void* dst, int voff, int soff = 0) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
 }
 
 template <int TM>
@@ -428,23 +428,44 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
     const int kr = blk * 2 + (lane >> 5);
     const int cb = b_chunk_swz(kr, lane & 31);
     // Columns past N never change with k: push such a chunk's row out of
-    // range once so the per-tile row test also covers them.
-    b_row[i] = (n0 + cb * 8 < g.N) ? kr : 0x3fffffff;
-    b_off[i] = (kr * g.ldb + n0 + cb * 8) * 2;
+    // range once so the per-tile row test also covers them, and point its
+    // offset at the end of B so the unchecked issue below reads zeros too.
+    const bool live = n0 + cb * 8 < g.N;
+    b_row[i] = live ? kr : 0x3fffffff;
+    b_off[i] = live ? (kr * g.ldb + n0 + cb * 8) * 2 : g.b_bytes;
   }
 
-  auto issue_tile = [&](auto sc, int kt) {
+  // The A part (kADma loads) or B part (4 loads) of tile kt into stage sc.
+  // Checked form (full = false): every chunk past K (A columns, B rows) or
+  // N is redirected past the buffer extent.  Unchecked form for tiles
+  // wholly inside K (k0 + 32 <= K): the per-lane offsets stay fixed and the
+  // K advance travels in the scalar offset, so the issue costs no vector
+  // instructions.  Rows past M (A) and columns past N (B) have lane offsets
+  // at or beyond the buffer extent on their own, so they read zeros whether
+  // or not the hardware range check counts the scalar offset; all sums stay
+  // below 2^32 (extents and K advances are below 2^31 each).
+  auto issue_a = [&](auto sc, auto full, int kt) {
     unsigned char* st = dma_stage<TM, decltype(sc)::value>();
     const int k0 = kt * kDmaK;
 #pragma unroll
     for (int i = 0; i < kADma; ++i) {
-      const int off = (k0 + a_col[i] < g.K) ? a_off[i] + k0 * 2 : kOobOffset;
-      dma16(rsrc_a, (lds_void*)(st + (wave * kADma + i) * 1024), off);
+      lds_void* dst = (lds_void*)(st + (wave * kADma + i) * 1024);
+      if constexpr (decltype(full)::value)
+        dma16(rsrc_a, dst, a_off[i], k0 * 2);
+      else
+        dma16(rsrc_a, dst, (k0 + a_col[i] < g.K) ? a_off[i] + k0 * 2 : kOobOffset);
     }
+  };
+  auto issue_b = [&](auto sc, auto full, int kt) {
+    unsigned char* st = dma_stage<TM, decltype(sc)::value>();
+    const int k0 = kt * kDmaK;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int off = (k0 + b_row[i] < g.K) ? b_off[i] + k0 * g.ldb * 2 : kOobOffset;
-      dma16(rsrc_b, (lds_void*)(st + kABytes + (wave * 4 + i) * 1024), off);
+      lds_void* dst = (lds_void*)(st + kABytes + (wave * 4 + i) * 1024);
+      if constexpr (decltype(full)::value)
+        dma16(rsrc_b, dst, b_off[i], k0 * g.ldb * 2);
+      else
+        dma16(rsrc_b, dst, (k0 + b_row[i] < g.K) ? b_off[i] + k0 * g.ldb * 2 : kOobOffset);
     }
   };
 
@@ -499,63 +520,89 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
   };
 
   constexpr int kReads = kMi + 8;  // LDS reads per 16-wide K step
+  constexpr int kMfmas = 4 * kMi;  // MFMAs per 16-wide K step
   u32x4 fa0[kMi], fb0[4], fa1[kMi], fb1[4];
 
-  // One K tile from stage S.  On entry fa0/fb0 hold its first 16-wide K
-  // step; on exit they hold the next tile's.
-  auto iteration = [&](auto sc, int kt) {
-    constexpr int S = decltype(sc)::value;
-    read_frags(sc, 1, fa1, fb1);
-    mfma_block(fa0, fb0);
-    // Issue the fragment reads early, between the first MFMAs.
+  // Instruction order of one 16-wide K step: fragment reads two at a time
+  // behind the first MFMAs, and nv DMA loads spread evenly over the step
+  // (bunched DMA issue stalls the wave on the address path).
+  auto schedule = [&](auto nv_c) {
+    constexpr int nv = decltype(nv_c)::value;
+    constexpr int stride = kMfmas / nv;
 #pragma unroll
-    for (int i = 0; i < kReads / 2; ++i) {
+    for (int m = 0; m < kMfmas; ++m) {
       __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+      if (2 * m < kReads) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+      if (m % stride == 1 && m / stride < nv) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSgMfma, 4 * kMi - kReads / 2, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    // Tile kt+1 has landed for this wave (later tiles may still be in
-    // flight); this wave's fragment reads of tile kt are complete.
-    wait_vmcnt<(STAGES - 3) * kDmaPerWave>();
-    wait_lgkm0();
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    // Every wave is past its reads of tile kt-1: its stage takes tile
-    // kt+STAGES-1 (tiles past K load zeros and are never multiplied).
-    issue_tile(StageC<(S + STAGES - 1) % STAGES>{}, kt + STAGES - 1);
-    read_frags(StageC<(S + 1) % STAGES>{}, 0, fa0, fb0);
-    mfma_block(fa1, fb1);
-#pragma unroll
-    for (int i = 0; i < kDmaPerWave; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 1, 0);
-      if (2 * i < kReads) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(kSgMfma, 4 * kMi - kDmaPerWave, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Prologue: tiles 0..STAGES-2 in flight; wait for tile 0.
-  issue_tile(StageC<0>{}, 0);
-  issue_tile(StageC<1>{}, 1);
-  if constexpr (STAGES == 4) issue_tile(StageC<2>{}, 2);
-  wait_vmcnt<(STAGES - 2) * kDmaPerWave>();
+  // One K tile from stage S.  On entry fa0/fb0 hold its first 16-wide K
+  // step; on exit they hold the next tile's.  A stage is refilled as soon
+  // as the barrier after its last fragment reads has passed: tile
+  // kt + STAGES goes into stage S, its A part after this tile's barrier
+  // and its B part before the next one.  kFull: both tiles requested here
+  // (B of kt + STAGES - 1, A of kt + STAGES) lie wholly inside K; tiles
+  // past K load zeros and are never multiplied.
+  auto iteration = [&](auto sc, auto full, int kt) {
+    constexpr int S = decltype(sc)::value;
+    read_frags(sc, 1, fa1, fb1);
+    issue_b(StageC<(S + STAGES - 1) % STAGES>{}, full, kt + STAGES - 1);
+    mfma_block(fa0, fb0);
+    schedule(std::integral_constant<int, 4>{});
+    // Tile kt+1 has landed for this wave (the two tiles requested after it
+    // may still be in flight); this wave's fragment reads of tile kt are
+    // complete.
+    wait_vmcnt<(STAGES - 2) * kDmaPerWave>();
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    // Every wave is past its reads of tile kt: stage S takes tile kt+STAGES.
+    read_frags(StageC<(S + 1) % STAGES>{}, 0, fa0, fb0);
+    issue_a(sc, full, kt + STAGES);
+    mfma_block(fa1, fb1);
+    schedule(std::integral_constant<int, kADma>{});
+  };
+
+  // Prologue: tiles 0..STAGES-2 and the A part of tile STAGES-1 in flight;
+  // wait for tile 0.
+  issue_a(StageC<0>{}, std::false_type{}, 0);
+  issue_b(StageC<0>{}, std::false_type{}, 0);
+  issue_a(StageC<1>{}, std::false_type{}, 1);
+  issue_b(StageC<1>{}, std::false_type{}, 1);
+  if constexpr (STAGES == 4) {
+    issue_a(StageC<2>{}, std::false_type{}, 2);
+    issue_b(StageC<2>{}, std::false_type{}, 2);
+  }
+  issue_a(StageC<STAGES - 1>{}, std::false_type{}, STAGES - 1);
+  wait_vmcnt<(STAGES - 2) * kDmaPerWave + kADma>();
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   read_frags(StageC<0>{}, 0, fa0, fb0);
 
+  using Full = std::true_type;
+  using Checked = std::false_type;
   int kt = 0;
-  for (; kt + STAGES <= nk; kt += STAGES) {
-    iteration(StageC<0>{}, kt);
-    iteration(StageC<1>{}, kt + 1);
-    iteration(StageC<2>{}, kt + 2);
-    if constexpr (STAGES == 4) iteration(StageC<3 % STAGES>{}, kt + 3);
+  // Trips whose requested tiles (kt + STAGES - 1 .. kt + 2 * STAGES - 1)
+  // all lie inside K, then the checked remainder.
+  const int nfull = g.K / kDmaK;
+  for (; kt + 2 * STAGES <= nfull; kt += STAGES) {
+    iteration(StageC<0>{}, Full{}, kt);
+    iteration(StageC<1>{}, Full{}, kt + 1);
+    iteration(StageC<2>{}, Full{}, kt + 2);
+    if constexpr (STAGES == 4) iteration(StageC<3 % STAGES>{}, Full{}, kt + 3);
   }
-  if (kt < nk) iteration(StageC<0>{}, kt++);
-  if (kt < nk) iteration(StageC<1>{}, kt++);
+  for (; kt + STAGES <= nk; kt += STAGES) {
+    iteration(StageC<0>{}, Checked{}, kt);
+    iteration(StageC<1>{}, Checked{}, kt + 1);
+    iteration(StageC<2>{}, Checked{}, kt + 2);
+    if constexpr (STAGES == 4) iteration(StageC<3 % STAGES>{}, Checked{}, kt + 3);
+  }
+  if (kt < nk) iteration(StageC<0>{}, Checked{}, kt++);
+  if (kt < nk) iteration(StageC<1>{}, Checked{}, kt++);
   if constexpr (STAGES == 4)
-    if (kt < nk) iteration(StageC<2>{}, kt++);
+    if (kt < nk) iteration(StageC<2>{}, Checked{}, kt++);
   // No DMA may still be writing LDS when the workgroup retires.
   wait_vmcnt<0>();
 

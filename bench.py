@@ -47,8 +47,10 @@ def log(msg: str) -> None:
 def parse_args() -> argparse.Namespace:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=100)
-    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=400)
+    p.add_argument("--min-warm-ms", type=float, default=60.0,
+                   help="keep warming up (untimed) until at least this much sustained load has run")
     p.add_argument("--workload", default="c2_4096_f16")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true")
@@ -77,12 +79,27 @@ def dtype_short(name: str) -> str:
     return {"float16": "f16", "bfloat16": "bf16"}[name]
 
 
+WARM_S = 0.06  # overwritten from --min-warm-ms in main()
+
+
 def time_launches(torch, stream, fn, steps: int, warmup: int) -> tuple[float, float]:
-    """(event seconds per launch, host seconds per step) over `steps` launches."""
+    """(event seconds per launch, host seconds per step) over `steps` launches.
+
+    Before timing: `warmup` launches, then more until WARM_S seconds of
+    sustained load have run.  Under a fresh load the board's clock needs
+    about 25 ms to settle (a 4096^3 launch takes ~165 us in the first
+    milliseconds and ~115 us after), so the timed launches measure the
+    sustained state."""
+    t_w = time.perf_counter()
     with torch.cuda.stream(stream):
         for _ in range(warmup):
             fn()
     torch.cuda.synchronize()
+    while time.perf_counter() - t_w < WARM_S:
+        with torch.cuda.stream(stream):
+            for _ in range(10):
+                fn()
+        torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -114,19 +131,24 @@ def cpu_baseline(cfg, a, b, target_s: float) -> dict:
         if elapsed >= target_s / 4 or rows >= cfg.m:
             break
         rows = min(cfg.m, max(rows * 2, int(rows * (target_s / 4) / max(elapsed, 1e-3))))
-    # One more run at the size that lands near the target, timed as the result.
+    # The timed sample: rows near the target size, repeated when even all
+    # rows of the workload finish well inside the target time.
     rows = min(cfg.m, max(16, int(rows * target_s / max(elapsed, 1e-3) / 2)))
+    reps = 1
+    if rows == cfg.m and elapsed * rows / max(1, len(idx)) < target_s / 2:
+        reps = max(1, int(target_s / max(elapsed * rows / len(idx), 1e-3)))
     idx = np.arange(rows, dtype=np.int64)
     t0 = time.perf_counter()
-    hc_oracle.gemm_c_rows(a, b, idx, dt, threads=threads)
+    for _ in range(reps):
+        hc_oracle.gemm_c_rows(a, b, idx, dt, threads=threads)
     elapsed = time.perf_counter() - t0
-    flops = 2.0 * rows * cfg.n * cfg.k
+    flops = 2.0 * rows * cfg.n * cfg.k * reps
     return {
         "value": flops / elapsed / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"rows 0..{rows - 1} of {cfg.name} ({rows}x{cfg.n}x{cfg.k}), {elapsed:.1f} s, "
+        "sample": f"rows 0..{rows - 1} of {cfg.name} ({rows}x{cfg.n}x{cfg.k}) x {reps}, {elapsed:.1f} s, "
         f"C oracle (sequential fp32 fold, OpenMP over row blocks) on {os.cpu_count()} host CPUs",
         "simulator_shape": simulator_shape_baseline(cfg),
     }
@@ -209,6 +231,8 @@ def bench_config(torch, g, stream, name: str, steps: int, warmup: int) -> dict:
 
 def main() -> int:
     args = parse_args()
+    global WARM_S
+    WARM_S = max(0.0, args.min_warm_ms) / 1e3
     if args.gpus != 1:
         print(
             f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X; "
@@ -286,6 +310,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "min_warm_ms": args.min_warm_ms,
         "ms_per_step": host_per_step * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
@@ -314,7 +339,7 @@ def main() -> int:
             if name in (cfg.name, "c4_skinny_f16"):
                 continue
             log(f"bench: {name}")
-            others[name] = bench_config(torch, g, stream, name, max(10, args.steps // 4), 5)
+            others[name] = bench_config(torch, g, stream, name, max(20, args.steps // 4), 5)
         result["others"] = others
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (oracle)")
