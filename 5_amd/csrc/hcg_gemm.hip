@@ -384,10 +384,12 @@ __device__ __forceinline__ int b_chunk_swz(int k, int c) {
   return c ^ ((m >> 1) * 10 + (m & 1) * 4);
 }
 
-template <int DT, int TM, int STAGES>
+template <int DT, int TM, int TN, int STAGES>
 __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_kernel(FastArgs g) {
   static_assert((TM == 256 && STAGES == 4) || (TM == 128 && STAGES == 3), "tile variant");
+  static_assert(TN == 256 || TN == 192 || TN == 128, "tile width");
   constexpr int kMi = TM / 64;            // 32-row MFMA tiles per wave
+  constexpr int kNi = TN / 64;            // 32-column MFMA tiles per wave
   constexpr int kADma = TM / 64;          // A DMA instructions per wave per stage
   constexpr int kDmaPerWave = kADma + 4;  // + 4 for B
   constexpr int kABytes = TM * kDmaK * 2;
@@ -401,7 +403,7 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
 
   int tm, tn;
   tile_coords(g.tiles_m, g.tiles_n, tm, tn);
-  const int m0 = tm * TM, n0 = tn * kTileN;
+  const int m0 = tm * TM, n0 = tn * TN;
   const int nk = (g.K + kDmaK - 1) / kDmaK;
 
   const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(g.A, g.a_bytes);
@@ -412,7 +414,8 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
   // row blk*16 + l/4 at physical chunk l%4, so it loads the logical chunk
   // that the swizzle puts there (the swizzles are XOR involutions).  B: wave
   // w owns 2-row blocks 4w..4w+3; lane l covers k row blk*2 + l/32 at
-  // physical chunk l%32.
+  // physical chunk l%32.  B rows in LDS are always 32 chunks (512 bytes);
+  // for TN < 256 the chunks past TN are dead and load zeros.
   int a_off[kADma], a_col[kADma], b_off[4], b_row[4];
 #pragma unroll
   for (int i = 0; i < kADma; ++i) {
@@ -430,7 +433,7 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
     // Columns past N never change with k: push such a chunk's row out of
     // range once so the per-tile row test also covers them, and point its
     // offset at the end of B so the unchecked issue below reads zeros too.
-    const bool live = n0 + cb * 8 < g.N;
+    const bool live = cb < TN / 8 && n0 + cb * 8 < g.N;
     b_row[i] = live ? kr : 0x3fffffff;
     b_off[i] = live ? (kr * g.ldb + n0 + cb * 8) * 2 : g.b_bytes;
   }
@@ -470,7 +473,7 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
   };
 
   // Fragment addresses (bytes within a stage).
-  int fa_addr[2][kMi], fb_addr[2][4][2];
+  int fa_addr[2][kMi], fb_addr[2][kNi][2];
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
@@ -480,23 +483,23 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
       fa_addr[kk][mi] = row * 64 + a_chunk_swz(row, c) * 16;
     }
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
+    for (int ni = 0; ni < kNi; ++ni) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int sl = lane & 15, grp = lane >> 4;
         const int krow = kk * 16 + 8 * (grp >> 1) + 4 * h + (sl >> 2);
-        const int ncol = wn * 128 + ni * 32 + 16 * (grp & 1) + 4 * (sl & 3);
+        const int ncol = wn * (TN / 2) + ni * 32 + 16 * (grp & 1) + 4 * (sl & 3);
         fb_addr[kk][ni][h] = kABytes + krow * 512 + b_chunk_swz(krow, ncol >> 3) * 16 + (ncol & 7) * 2;
       }
     }
   }
 
-  auto read_frags = [&](auto sc, int kk, u32x4 (&fa)[kMi], u32x4 (&fb)[4]) {
+  auto read_frags = [&](auto sc, int kk, u32x4 (&fa)[kMi], u32x4 (&fb)[kNi]) {
     const unsigned char* st = dma_stage<TM, decltype(sc)::value>();
 #pragma unroll
     for (int mi = 0; mi < kMi; ++mi) fa[mi] = *reinterpret_cast<const u32x4*>(st + fa_addr[kk][mi]);
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
+    for (int ni = 0; ni < kNi; ++ni) {
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (__attribute__((address_space(3))) s16x4*)(st + fb_addr[kk][ni][0]));
       const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -506,34 +509,41 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
     }
   };
 
-  f32x16 acc[kMi][4];
+  f32x16 acc[kMi][kNi];
 #pragma unroll
   for (int i = 0; i < kMi; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < kNi; ++j) acc[i][j] = f32x16{};
 
-  auto mfma_block = [&](const u32x4 (&fa)[kMi], const u32x4 (&fb)[4]) {
+  auto mfma_block = [&](const u32x4 (&fa)[kMi], const u32x4 (&fb)[kNi]) {
 #pragma unroll
     for (int mi = 0; mi < kMi; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma32x32x16<DT>(fa[mi], fb[ni], acc[mi][ni]);
+      for (int ni = 0; ni < kNi; ++ni) acc[mi][ni] = mfma32x32x16<DT>(fa[mi], fb[ni], acc[mi][ni]);
   };
 
-  constexpr int kReads = kMi + 8;  // LDS reads per 16-wide K step
-  constexpr int kMfmas = 4 * kMi;  // MFMAs per 16-wide K step
-  u32x4 fa0[kMi], fb0[4], fa1[kMi], fb1[4];
+  constexpr int kReads = kMi + 2 * kNi;  // LDS reads per 16-wide K step
+  constexpr int kMfmas = kMi * kNi;      // MFMAs per 16-wide K step
+  u32x4 fa0[kMi], fb0[kNi], fa1[kMi], fb1[kNi];
 
   // Instruction order of one 16-wide K step: fragment reads two at a time
   // behind the first MFMAs, and nv DMA loads spread evenly over the step
   // (bunched DMA issue stalls the wave on the address path).
+  // DMA load v of nv goes behind MFMA slot v*kMfmas/nv (+1 when the slots
+  // are at least two apart, so the first load does not share the first
+  // slot with two fragment reads).
   auto schedule = [&](auto nv_c) {
     constexpr int nv = decltype(nv_c)::value;
-    constexpr int stride = kMfmas / nv;
+    constexpr int shift = kMfmas >= 2 * nv ? 1 : 0;
 #pragma unroll
     for (int m = 0; m < kMfmas; ++m) {
       __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
       if (2 * m < kReads) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
-      if (m % stride == 1 && m / stride < nv) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 1, 0);
+      int loads = 0;
+#pragma unroll
+      for (int v = 0; v < nv; ++v) loads += (v * kMfmas / nv + shift == m) ? 1 : 0;
+      if (loads == 1) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 1, 0);
+      if (loads == 2) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 2, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -618,36 +628,49 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
   constexpr int kEpRow = 136;     // floats per staged row
   float* ep = reinterpret_cast<float*>((wave < 2 ? dma_stage<TM, 0>() : dma_stage<TM, 1>()) +
                                        (wave & 1) * (16 * kEpRow * 4));
-  const bool full = g.c_vec && (m0 + TM <= g.M) && (n0 + kTileN <= g.N);
+  const bool full = g.c_vec && (m0 + TM <= g.M) && (n0 + TN <= g.N);
   const int col_l = lane & 31;
   const int row_l = (lane >> 5) * 4;
   const int c4 = (lane & 31) * 4;
-  const int gcol = n0 + wn * 128 + c4;
+  const int gcol = n0 + wn * (TN / 2) + c4;
+  const bool col_live = c4 < TN / 2;  // lanes past the wave's TN/2 columns store nothing
 #pragma unroll
   for (int mi = 0; mi < kMi; ++mi) {
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
-      for (int ni = 0; ni < 4; ++ni)
+      for (int ni = 0; ni < kNi; ++ni)
 #pragma unroll
         for (int r = 8 * hh; r < 8 * hh + 8; ++r)
           ep[(((r >> 2) & 1) * 8 + row_l + (r & 3)) * kEpRow + ni * 32 + col_l] = acc[mi][ni][r];
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // Lane l stores columns 4*(l%32) .. +3 of staged rows 2*i + l/32.
+      if (full) {
+        // Lane l stores columns 4*(l%32) .. +3 of staged rows 2*i + l/32.
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int lr = 2 * i + (lane >> 5);
-        const f32x4 v = *reinterpret_cast<const f32x4*>(ep + lr * kEpRow + c4);
-        const int grow = m0 + wm * (TM / 2) + mi * 32 + hh * 16 + lr;
-        float* dst = g.C + (int64_t)grow * g.ldc + gcol;
-        if (full) {
-          __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst));
-        } else if (grow < g.M) {
+        for (int i = 0; i < 8; ++i) {
+          const int lr = 2 * i + (lane >> 5);
+          const f32x4 v = *reinterpret_cast<const f32x4*>(ep + lr * kEpRow + c4);
+          const int grow = m0 + wm * (TM / 2) + mi * 32 + hh * 16 + lr;
+          float* dst = g.C + (int64_t)grow * g.ldc + gcol;
+          if (col_live) __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst));
+        }
+      } else {
+        // Edge tiles and C rows without 16-byte alignment: 4-byte stores,
+        // lane l at column l%32 + 32e, so each store covers 128 contiguous
+        // bytes of two rows.
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (gcol + e < g.N) dst[e] = v[e];
+        for (int i = 0; i < 8; ++i) {
+          const int lr = 2 * i + (lane >> 5);
+          const int grow = m0 + wm * (TM / 2) + mi * 32 + hh * 16 + lr;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int lc = col_l + 32 * e;
+            const float v = ep[lr * kEpRow + lc];
+            const int gc = n0 + wn * (TN / 2) + lc;
+            if (lc < TN / 2 && grow < g.M && gc < g.N) g.C[(int64_t)grow * g.ldc + gc] = v;
+          }
         }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -669,52 +692,73 @@ struct RepackJob {
   int64_t chunks;  // rows * ld_out / 8
 };
 
-// One 8-element output chunk.  A chunk that lies inside the row is read as
-// aligned 4-byte words: 4 words when its first element starts a word, else 5
-// words and a 16-bit funnel shift.  The first and last words read each hold
-// an element of the chunk, so no read leaves the words that hold valid
-// data.  The row's final, partial chunk is read element by element.
-__device__ __forceinline__ void repack_chunk(const RepackJob& j, int64_t idx) {
-  const int64_t per_row = j.ld_out / 8;
-  const int row = (int)(idx / per_row);
-  const int c0 = (int)(idx % per_row) * 8;
-  const int64_t f = (int64_t)row * j.ld + c0;  // flat source element index
-  uint32_t w[4];
-  if (c0 + 8 <= j.cols) {
-    // Element index counted from the 4-byte boundary at or below src.
-    const int off = (int)((reinterpret_cast<uintptr_t>(j.src) >> 1) & 1);
-    const int64_t g = f + off;
-    const uint32_t* q =
-        reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(j.src) - 2 * off) + (g >> 1);
-    if ((g & 1) == 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) w[i] = q[i];
-    } else {
-      uint32_t v[5];
-#pragma unroll
-      for (int i = 0; i < 5; ++i) v[i] = q[i];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) w[i] = (v[i] >> 16) | (v[i + 1] << 16);
-    }
-  } else {
-    const uint16_t* p = j.src + f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = c0 + 2 * i;
-      const uint32_t lo = c < j.cols ? p[2 * i] : 0u;
-      const uint32_t hi = c + 1 < j.cols ? p[2 * i + 1] : 0u;
-      w[i] = lo | (hi << 16);
-    }
-  }
-  *reinterpret_cast<u32x4*>(j.dst + (int64_t)row * j.ld_out + c0) = u32x4{w[0], w[1], w[2], w[3]};
-}
+// Each thread writes four 8-element output chunks, 256 chunks apart; the
+// source words of all four are gathered before any is shifted and stored,
+// so that the thread has their loads in flight at once.  A chunk that lies
+// inside its row is read as aligned 4-byte words: 4 words when its first
+// element starts a word, else 5 words and a 16-bit funnel shift.  The first
+// and last words read each hold an element of the chunk, so no read leaves
+// the words that hold valid data.  The row's final, partial chunk is read
+// element by element.
+constexpr int kRepackPer = 4;
 
 __global__ __launch_bounds__(256) void repack_kernel(RepackJob a, RepackJob b) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx < a.chunks) {
-    repack_chunk(a, idx);
-  } else if (idx - a.chunks < b.chunks) {
-    repack_chunk(b, idx - a.chunks);
+  const int64_t base = (int64_t)blockIdx.x * (256 * kRepackPer) + threadIdx.x;
+  uint32_t w[kRepackPer][5];
+  uint16_t* dst[kRepackPer];
+  int mode[kRepackPer];  // 0: 4 aligned words, 1: 5 words + shift, 2: partial row end, 3: none
+#pragma unroll
+  for (int i = 0; i < kRepackPer; ++i) {
+    int64_t idx = base + 256 * i;
+    const bool in_a = idx < a.chunks;
+    if (!in_a) idx -= a.chunks;
+    mode[i] = 3;
+    dst[i] = nullptr;
+#pragma unroll
+    for (int e = 0; e < 5; ++e) w[i][e] = 0;
+    if (!in_a && idx >= b.chunks) continue;
+    const uint16_t* src = in_a ? a.src : b.src;
+    const int64_t ld = in_a ? a.ld : b.ld;
+    const int cols = in_a ? a.cols : b.cols;
+    const int ld_out = in_a ? a.ld_out : b.ld_out;
+    // chunks < 2^27 (a repacked operand stays below 2^31 bytes), so 32-bit
+    // division suffices.
+    const uint32_t per_row = (uint32_t)ld_out / 8;
+    const int row = (int)((uint32_t)idx / per_row);
+    const int c0 = (int)((uint32_t)idx - (uint32_t)row * per_row) * 8;
+    const int64_t f = (int64_t)row * ld + c0;  // flat source element index
+    dst[i] = (in_a ? a.dst : b.dst) + (int64_t)row * ld_out + c0;
+    if (c0 + 8 <= cols) {
+      // Element index counted from the 4-byte boundary at or below src.
+      const int off = (int)((reinterpret_cast<uintptr_t>(src) >> 1) & 1);
+      const int64_t g = f + off;
+      const uint32_t* q =
+          reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(src) - 2 * off) + (g >> 1);
+      mode[i] = (int)(g & 1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[i][e] = q[e];
+      if (mode[i]) w[i][4] = q[4];
+    } else {
+      mode[i] = 2;
+      const uint16_t* p = src + f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c = c0 + 2 * e;
+        const uint32_t lo = c < cols ? p[2 * e] : 0u;
+        const uint32_t hi = c + 1 < cols ? p[2 * e + 1] : 0u;
+        w[i][e] = lo | (hi << 16);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kRepackPer; ++i) {
+    if (mode[i] == 3) continue;
+    u32x4 out{w[i][0], w[i][1], w[i][2], w[i][3]};
+    if (mode[i] == 1) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[e] = (w[i][e] >> 16) | (w[i][e + 1] << 16);
+    }
+    *reinterpret_cast<u32x4*>(dst[i]) = out;
   }
 }
 
@@ -1233,13 +1277,53 @@ int launch_generic(const TiledArgs& a, bool vec_a, bool vec_b, hipStream_t strea
   return HCG_OK;
 }
 
+// Output tile shapes of the DMA kernel.  TM = 256: 4-stage ring, one
+// workgroup per CU; TM = 128: 3-stage ring, two workgroups per CU.
+struct TileShape {
+  int tm, tn;
+  int per_cu;   // workgroups resident per CU
+  float eff;    // relative MFMA issue efficiency of the K loop (measured)
+};
+constexpr TileShape kTileShapes[] = {
+    {256, 256, 1, 1.00f},
+    {256, 192, 1, 0.97f},
+    {128, 256, 2, 0.93f},
+    {128, 128, 2, 0.80f},
+};
+constexpr int kNumTileShapes = sizeof(kTileShapes) / sizeof(kTileShapes[0]);
+
+// Picks the tile shape with the least modelled time: the busiest CU's
+// share of tiles times tile area times K steps (scaled by the shape's K-loop
+// efficiency), plus a fixed cost per round of resident workgroups
+// (prologue, epilogue, launch), worth about six 256x256 K tiles.
+int pick_tile_shape(int num_cus, int M, int N, int K) {
+  const double nk = (double)((K + kDmaK - 1) / kDmaK);
+  int best = 0;
+  double best_cost = 0;
+  for (int i = 0; i < kNumTileShapes; ++i) {
+    const TileShape& t = kTileShapes[i];
+    const int64_t tiles = (int64_t)((M + t.tm - 1) / t.tm) * ((N + t.tn - 1) / t.tn);
+    if (tiles > 0x7fffffff) continue;
+    const int64_t per_cu = (tiles + num_cus - 1) / num_cus;
+    const int64_t rounds = (per_cu + t.per_cu - 1) / t.per_cu;
+    const double cost = (double)per_cu * t.tm * t.tn * nk / t.eff + (double)rounds * 6.0 * 256 * 256;
+    if (best_cost == 0 || cost < best_cost) {
+      best = i;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 template <int DT>
-int launch_dma(const FastArgs& a, int tile_m, hipStream_t stream) {
+int launch_dma(const FastArgs& a, int shape, hipStream_t stream) {
   const dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
-  if (tile_m == 256) {
-    gemm_dma_kernel<DT, 256, 4><<<grid, dim3(kTiledThreads), 0, stream>>>(a);
-  } else {
-    gemm_dma_kernel<DT, 128, 3><<<grid, dim3(kTiledThreads), 0, stream>>>(a);
+  const dim3 block(kTiledThreads);
+  switch (shape) {
+    case 0: gemm_dma_kernel<DT, 256, 256, 4><<<grid, block, 0, stream>>>(a); break;
+    case 1: gemm_dma_kernel<DT, 256, 192, 4><<<grid, block, 0, stream>>>(a); break;
+    case 2: gemm_dma_kernel<DT, 128, 256, 3><<<grid, block, 0, stream>>>(a); break;
+    default: gemm_dma_kernel<DT, 128, 128, 3><<<grid, block, 0, stream>>>(a); break;
   }
   HCG_HIP_CHECK(hipGetLastError());
   return HCG_OK;
@@ -1410,7 +1494,8 @@ int64_t fast_extent_b(int N, int K, int64_t ldb) {
 }
 
 int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
-              float* C, int64_t ldc, int M, int N, int K, hipStream_t stream, bool force_generic) {
+              float* C, int64_t ldc, int M, int N, int K, hipStream_t stream, bool force_generic,
+              int force_shape) {
   const int64_t kLimit = (int64_t)1 << 31;
   // The DMA kernel masks at 8-element granularity, so it also needs K and N
   // to be multiples of 8 (or zero padding supplied by a repack).
@@ -1444,7 +1529,8 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
       b_use = b_p;
     }
     const int64_t n = ja.chunks + jb.chunks;
-    repack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(ja, jb);
+    const int64_t per_block = 256 * kRepackPer;
+    repack_kernel<<<(unsigned)((n + per_block - 1) / per_block), 256, 0, stream>>>(ja, jb);
     HCG_HIP_CHECK(hipGetLastError());
   }
   FastArgs f{};
@@ -1457,26 +1543,25 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
   f.M = M;
   f.N = N;
   f.K = K;
-  // 256-row tiles when they fill the chip (one workgroup per CU); otherwise
-  // 128-row tiles, two workgroups per CU.
-  const int64_t tiles256 = (int64_t)((M + 255) / 256) * ((N + kTileN - 1) / kTileN);
-  const int tile_m = tiles256 >= st->num_cus ? 256 : 128;
-  f.tiles_m = (M + tile_m - 1) / tile_m;
-  f.tiles_n = (N + kTileN - 1) / kTileN;
+  const int shape = force_shape >= 0 ? force_shape : pick_tile_shape(st->num_cus, M, N, K);
+  const TileShape& ts = kTileShapes[shape];
+  if ((int64_t)((M + ts.tm - 1) / ts.tm) * ((N + ts.tn - 1) / ts.tn) > 0x7fffffff)
+    return run_generic(dtype, A, lda, B, ldb, C, ldc, M, N, K, stream);
+  f.tiles_m = (M + ts.tm - 1) / ts.tm;
+  f.tiles_n = (N + ts.tn - 1) / ts.tn;
   // Range-check extents cover the last valid element, rounded up to the
   // 16-byte chunk that holds it (never past that chunk).
   f.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda_p + K) * 2, 16);
   f.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * ldb_p + N) * 2, 16);
   f.c_vec = aligned16(C) && ldc % 4 == 0;
-  return dtype == HCG_F16 ? launch_dma<HCG_F16>(f, tile_m, stream) : launch_dma<HCG_BF16>(f, tile_m, stream);
+  return dtype == HCG_F16 ? launch_dma<HCG_F16>(f, shape, stream) : launch_dma<HCG_BF16>(f, shape, stream);
 }
 
 int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
               float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream_ptr) {
   if (dtype != HCG_F16 && dtype != HCG_BF16)
     return set_error(HCG_EINVAL, "dtype must be HCG_F16 (0) or HCG_BF16 (1), got %d", dtype);
-  if (algo != HCG_ALGO_AUTO && algo != HCG_ALGO_TILED && algo != HCG_ALGO_SKINNY &&
-      algo != HCG_ALGO_GENERIC)
+  if (algo < HCG_ALGO_AUTO || algo > HCG_ALGO_TILED_128x128)
     return set_error(HCG_EINVAL, "unknown algo %d", algo);
   if (M < 0 || N < 0 || K < 0)
     return set_error(HCG_EINVAL, "negative extent: M=%lld N=%lld K=%lld", (long long)M,
@@ -1515,8 +1600,9 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
   if (use_skinny) {
     rc = run_skinny(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream);
   } else {
+    const int force_shape = algo >= HCG_ALGO_TILED_256x256 ? algo - HCG_ALGO_TILED_256x256 : -1;
     rc = run_tiled(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream,
-                   algo == HCG_ALGO_GENERIC);
+                   algo == HCG_ALGO_GENERIC, force_shape);
   }
   if (rc == HCG_OK) t_last_error.clear();
   return rc;

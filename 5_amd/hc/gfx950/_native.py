@@ -31,8 +31,21 @@ HCG_ALGO_AUTO = 0
 HCG_ALGO_TILED = 1
 HCG_ALGO_SKINNY = 2
 HCG_ALGO_GENERIC = 3
+HCG_ALGO_TILED_256x256 = 4
+HCG_ALGO_TILED_256x192 = 5
+HCG_ALGO_TILED_128x256 = 6
+HCG_ALGO_TILED_128x128 = 7
 
-ALGOS = {"auto": HCG_ALGO_AUTO, "tiled": HCG_ALGO_TILED, "skinny": HCG_ALGO_SKINNY, "generic": HCG_ALGO_GENERIC}
+ALGOS = {
+    "auto": HCG_ALGO_AUTO,
+    "tiled": HCG_ALGO_TILED,
+    "skinny": HCG_ALGO_SKINNY,
+    "generic": HCG_ALGO_GENERIC,
+    "tiled_256x256": HCG_ALGO_TILED_256x256,
+    "tiled_256x192": HCG_ALGO_TILED_256x192,
+    "tiled_128x256": HCG_ALGO_TILED_128x256,
+    "tiled_128x128": HCG_ALGO_TILED_128x128,
+}
 
 # Every symbol include/hcg_gemm.h declares.
 EXPORTS = ("hcg_init", "hcg_gemm", "hcg_gemm_algo", "hcg_last_error", "hcg_version")

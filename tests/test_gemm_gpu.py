@@ -167,6 +167,37 @@ def test_large_tile_variant_integer_bit_exact():
     assert np.array_equal(got, (ai @ bi).astype(np.float32))
 
 
+TILE_ALGOS = ["tiled_256x256", "tiled_256x192", "tiled_128x256", "tiled_128x128"]
+
+
+@pytest.mark.parametrize("algo", TILE_ALGOS)
+@pytest.mark.parametrize("m,n,k", [(17, 19, 18), (255, 257, 33), (520, 400, 1027), (1000, 3001, 264),
+                                   (768, 768, 4096)])
+def test_tile_shapes_tails(algo, m, n, k):
+    """Every output tile shape of the LDS-tiled kernel, forced, on ragged
+    M/N/K (K past and within one 32-wide tile, unaligned rows) and on a
+    shape where every K tile takes the unchecked load path."""
+    from hc.gfx950.workloads import make_inputs
+
+    print(f"case {algo} m={m} n={n} k={k}", flush=True)
+    a, b = make_inputs("c2_4096_f16", seed=m + 3 * n + k, m=m, n=n, k=k)
+    _check(_gemm(a, b, algo), oracle.gemm_c(a, b), k)
+
+
+@pytest.mark.parametrize("algo", TILE_ALGOS)
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_tile_shapes_integer_bit_exact(algo, dtype):
+    rng = np.random.default_rng(11)
+    ai = rng.integers(-4, 5, size=(600, 1024))
+    bi = rng.integers(-4, 5, size=(1024, 712))
+    if dtype == "float16":
+        a, b = ai.astype(np.float16), bi.astype(np.float16)
+    else:
+        a, b = oracle.f32_to_bf16_bits(ai.astype(np.float32)), oracle.f32_to_bf16_bits(bi.astype(np.float32))
+    print(f"case integer {algo} {dtype}", flush=True)
+    assert np.array_equal(_gemm(a, b, algo, dtype), (ai @ bi).astype(np.float32))
+
+
 @pytest.mark.parametrize("m,n,k", [(17, 19, 18), (300, 520, 200), (1000, 1000, 1000), (2048, 512, 3000)])
 def test_tails_bf16(m, n, k):
     from hc.gfx950.workloads import make_inputs
@@ -211,7 +242,8 @@ def test_runs_are_bit_identical(algo, m):
         assert np.array_equal(first.view(np.uint32), _gemm(a, b, algo).view(np.uint32))
 
 
-def test_strided_views_and_guard_band():
+@pytest.mark.parametrize("algo", ["auto"] + TILE_ALGOS)
+def test_strided_views_and_guard_band(algo):
     """A and B as column-sliced views (lda > K, ldb > N, 2-byte aligned
     starts), C as a view into a NaN-filled buffer: only C's M x N elements
     change (hc/simulator.py:1441-1458 writes only in-bounds C)."""
@@ -227,7 +259,8 @@ def test_strided_views_and_guard_band():
     vb.copy_(_dev(b))
     guard = torch.full((m + 2, n + 7), float("nan"), dtype=torch.float32, device=DEV)
     vc = guard[1 : m + 1, 2 : n + 2]
-    g.gemm(va, vb, out=vc)
+    print(f"case guard band {algo}", flush=True)
+    g.gemm(va, vb, out=vc, algo=algo)
     torch.cuda.synchronize()
     host = guard.cpu().numpy()
     _check(host[1 : m + 1, 2 : n + 2], oracle.gemm_c(a, b), k)
