@@ -35,7 +35,7 @@ def flags() -> list[str]:
     return [
         f"--offload-arch={ARCH}",
         "-O3",
-        "-std=c++17",
+        "-std=c++20",
         "-fPIC",
         "-shared",
         # Packed fp32 VALU forms stay disabled for all device code.

@@ -961,8 +961,20 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nb = blockIdx.x;
-  const int split = blockIdx.y;
+  // Workgroup -> (column block, split).  Workgroups are dispatched
+  // round-robin over the 8 XCDs (id % 8); the mapping gives every XCD, in
+  // every split, column blocks of all 8 residues mod 8, so that no XCD
+  // streams a fixed subset of B's 256-byte column positions.
+  int nb, split;
+  {
+    const int id = blockIdx.x;
+    const int per_split = gridDim.x / g.splits;  // column blocks (padded to a multiple of 8)
+    split = id / per_split;
+    const int r = id - split * per_split;
+    const int x = r & 7, q = r >> 3;
+    nb = 8 * q + ((x + q + split) & 7);
+  }
+  if (nb * NB >= g.N) return;
   const int n0 = nb * NB;
   const int kbeg = split * g.kchunk;
   const int kend = min(g.K, kbeg + g.kchunk);
@@ -1387,7 +1399,10 @@ int stream_splits(const DeviceState* st, int nblocks, int K) {
 
 template <int DT>
 int launch_stream(const StreamArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)((a.N + kStN - 1) / kStN), (unsigned)a.splits);
+  // Column blocks padded to a multiple of 8 per split (see the workgroup
+  // mapping in gemm_stream_kernel); padding workgroups exit at once.
+  const int nblocks = (a.N + kStN - 1) / kStN;
+  const dim3 grid((unsigned)(round_up(nblocks, 8) * a.splits));
   gemm_stream_kernel<DT><<<grid, dim3(256), 0, stream>>>(a);
   HCG_HIP_CHECK(hipGetLastError());
   if (a.splits > 1) {

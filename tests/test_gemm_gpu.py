@@ -217,6 +217,34 @@ def test_skinny(m, n, k):
     _check(_gemm(a, b, "skinny"), oracle.gemm_c(a, b), k)
 
 
+@pytest.mark.parametrize("m,n,k", [(16, 1000, 1000), (3, 8192, 520), (16, 4104, 8192), (7, 64, 4096),
+                                   (16, 65536, 4096), (16, 128, 256)])
+def test_skinny_split_and_block_mapping(m, n, k):
+    """The streaming kernel's split-K and workgroup-to-column-block mapping:
+    column-block counts that are not multiples of 8 (padding workgroups),
+    ragged last splits, one split (C written directly) and many blocks."""
+    from hc.gfx950.workloads import make_inputs
+
+    print(f"case skinny mapping m={m} n={n} k={k}", flush=True)
+    a, b = make_inputs("c4_skinny_f16", seed=m + n + 5 * k, m=m, n=n, k=k)
+    _check(_gemm(a, b, "skinny"), oracle.gemm_c(a, b), k)
+
+
+def test_skinny_repeated_launches_alternating_shapes():
+    """The per-stream workspace is reused across launches of different
+    shapes: each result matches the oracle, and the same input gives the
+    same bits again."""
+    from hc.gfx950.workloads import make_inputs
+
+    big = make_inputs("c4_skinny_f16", seed=21, m=16, n=8192, k=8192)
+    small = make_inputs("c4_skinny_f16", seed=22, m=16, n=1024, k=2048)
+    first = _gemm(*big, "skinny")
+    _check(first, oracle.gemm_c(*big), 8192)
+    _check(_gemm(*small, "skinny"), oracle.gemm_c(*small), 2048)
+    again = _gemm(*big, "skinny")
+    assert np.array_equal(first.view(np.uint32), again.view(np.uint32))
+
+
 @pytest.mark.parametrize("algo,m", [("tiled", 300), ("skinny", 16), ("generic", 300)])
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_integer_inputs_bit_exact(algo, m, dtype):
