@@ -2,8 +2,9 @@
 
     python 5_amd/csrc/build.py [-v]
 
-compiles 5_amd/csrc/hcg_gemm.hip (kernels + the C ABI declared in
-include/hcg_gemm.h) with hipcc for gfx950 into
+compiles 5_amd/csrc/hcg_gemm.hip and hcg_tile.hip (kernels + the C ABI
+declared in include/hcg_gemm.h and include/hcg_tile_ops.h) with hipcc for
+gfx950 into
 5_amd/hc/gfx950/libhcg_gfx950.so, next to the Python code that loads it.
 hipcc cross-compiles, so this runs on a machine without a GPU.
 """
@@ -18,7 +19,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
-SRC = os.path.join(HERE, "hcg_gemm.hip")
+SRCS = [os.path.join(HERE, "hcg_gemm.hip"), os.path.join(HERE, "hcg_tile.hip")]
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(PKG, "hc", "gfx950", "libhcg_gfx950.so")
 ARCH = "gfx950"
@@ -51,7 +52,7 @@ def flags() -> list[str]:
 def build(verbose: bool = False) -> str:
     os.makedirs(os.path.dirname(OUT), exist_ok=True)
     tmp = OUT + ".tmp"
-    cmd = [hipcc(), *flags(), SRC, "-o", tmp]
+    cmd = [hipcc(), *flags(), *SRCS, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)

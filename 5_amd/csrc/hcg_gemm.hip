@@ -39,8 +39,33 @@
 #include <string>
 
 #include "hcg_gemm.h"
+#include "hcg_runtime.h"
+#include "hcg_tile.h"
+
+namespace hcg {
+
+thread_local std::string t_last_error;
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  t_last_error = buf;
+  return code;
+}
+
+}  // namespace hcg
 
 namespace {
+
+using hcg::dma16;
+using hcg::dma_offset;
+using hcg::kOobOffset;
+using hcg::lds_void;
+using hcg::load_row8_u16;
+using hcg::make_rsrc;
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -75,25 +100,6 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
-}
-
-// 8 consecutive 16-bit elements of one row, starting at column col0; columns
-// at or beyond ncols read as +0 (the masked tile load of
-// hc/simulator.py:1338-1357 followed by with_inactive(0)).  kVec: the row is
-// 16-byte aligned at every multiple of 8 columns, so a whole in-bounds chunk
-// is one 128-bit load.
-template <bool kVec>
-__device__ __forceinline__ u32x4 load8(const uint16_t* rowp, int col0, int ncols) {
-  if (kVec && col0 + 8 <= ncols) return *reinterpret_cast<const u32x4*>(rowp + col0);
-  uint32_t w[4];
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int c = col0 + 2 * p;
-    const uint32_t lo = (c < ncols) ? rowp[c] : 0u;
-    const uint32_t hi = (c + 1 < ncols) ? rowp[c + 1] : 0u;
-    w[p] = lo | (hi << 16);
-  }
-  return u32x4{w[0], w[1], w[2], w[3]};
 }
 
 // 8x8 transpose of 16-bit elements held as 8 rows of 128 bits: on return
@@ -197,7 +203,7 @@ __global__ __launch_bounds__(kTiledThreads) void gemm_generic_kernel(TiledArgs g
       if (a_full) {
         ra[i] = *reinterpret_cast<const u32x4*>(p + k0 + a_c * 8);
       } else {
-        ra[i] = (row < g.M) ? load8<kVecA>(p, k0 + a_c * 8, g.K) : u32x4{0, 0, 0, 0};
+        ra[i] = (row < g.M) ? load_row8_u16<kVecA>(p, k0 + a_c * 8, g.K) : u32x4{0, 0, 0, 0};
       }
     }
 #pragma unroll
@@ -207,7 +213,7 @@ __global__ __launch_bounds__(kTiledThreads) void gemm_generic_kernel(TiledArgs g
       if (b_full) {
         rb[i] = *reinterpret_cast<const u32x4*>(p + n0 + b_n * 8);
       } else {
-        rb[i] = (k < g.K) ? load8<kVecB>(p, n0 + b_n * 8, g.N) : u32x4{0, 0, 0, 0};
+        rb[i] = (k < g.K) ? load_row8_u16<kVecB>(p, n0 + b_n * 8, g.N) : u32x4{0, 0, 0, 0};
       }
     }
   };
@@ -282,12 +288,6 @@ struct FastArgs {
   bool c_vec;            // C rows are 16-byte aligned at every 4th column
 };
 
-// Raw buffer resource: base, no swizzle/stride, `bytes` records.  Loads at or
-// beyond `bytes` return 0 (the hardware range check).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
-}
-
 // Scheduling-group masks for __builtin_amdgcn_sched_group_barrier.
 constexpr int kSgMfma = 0x008;
 constexpr int kSgVmemRead = 0x020;
@@ -318,10 +318,8 @@ constexpr int kSgDsRead = 0x100;
 // range check returns zeros; rows past M (A) or K (B) are past it already.
 
 constexpr int kDmaK = 32;
-constexpr int kOobOffset = 0x7ffffff0;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
 
 // s_waitcnt with only vmcnt (lgkmcnt / expcnt left at their maxima).
 template <int N>
@@ -330,10 +328,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
 }
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
-
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, lds_void* dst, int voff, int soff = 0) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
-}
 
 template <int TM>
 constexpr int dma_stage_bytes() {
@@ -456,7 +450,7 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
       if constexpr (decltype(full)::value)
         dma16(rsrc_a, dst, a_off[i], k0 * 2);
       else
-        dma16(rsrc_a, dst, (k0 + a_col[i] < g.K) ? a_off[i] + k0 * 2 : kOobOffset);
+        dma16(rsrc_a, dst, dma_offset(k0 + a_col[i] < g.K, a_off[i] + k0 * 2));
     }
   };
   auto issue_b = [&](auto sc, auto full, int kt) {
@@ -468,7 +462,7 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
       if constexpr (decltype(full)::value)
         dma16(rsrc_b, dst, b_off[i], k0 * g.ldb * 2);
       else
-        dma16(rsrc_b, dst, (k0 + b_row[i] < g.K) ? b_off[i] + k0 * g.ldb * 2 : kOobOffset);
+        dma16(rsrc_b, dst, dma_offset(k0 + b_row[i] < g.K, b_off[i] + k0 * g.ldb * 2));
     }
   };
 
@@ -788,7 +782,7 @@ __device__ __forceinline__ void skinny_load(const SkinnyArgs& g, int k0, int lan
   const int grp = lane >> 4;
   const int kr = k0 + grp * 8;
   const int arow = lane & 15;
-  af = (arow < g.M) ? load8<kVecA>(g.A + (int64_t)arow * g.lda, kr, g.K) : u32x4{0, 0, 0, 0};
+  af = (arow < g.M) ? load_row8_u16<kVecA>(g.A + (int64_t)arow * g.lda, kr, g.K) : u32x4{0, 0, 0, 0};
   const bool full = kVecB && (k0 + kSkinnyStep <= g.K) && (ncol0 + 8 <= g.N);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -797,7 +791,7 @@ __device__ __forceinline__ void skinny_load(const SkinnyArgs& g, int k0, int lan
     if (full) {
       rb[i] = *reinterpret_cast<const u32x4*>(p + ncol0);
     } else {
-      rb[i] = (k < g.K) ? load8<kVecB>(p, ncol0, g.N) : u32x4{0, 0, 0, 0};
+      rb[i] = (k < g.K) ? load_row8_u16<kVecB>(p, ncol0, g.N) : u32x4{0, 0, 0, 0};
     }
   }
 }
@@ -1007,11 +1001,11 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
     const int k0 = kbeg + step * kStStep;
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
-      const int off = (k0 + b_row[i] < kend) ? b_off[i] + k0 * g.ldb * 2 : kOobOffset;
+      const int off = dma_offset(k0 + b_row[i] < kend, b_off[i] + k0 * g.ldb * 2);
       dma16(rsrc_b, (lds_void*)(st_b<S>() + (wave * kDmaPerWave + i) * 1024), off);
     }
     if (wave == 0) {
-      const int off = (a_ok && k0 + a_c * 8 < kend) ? a_off + k0 * 2 : kOobOffset;
+      const int off = dma_offset(a_ok && k0 + a_c * 8 < kend, a_off + k0 * 2);
       dma16(rsrc_a, (lds_void*)st_a<S>(), off);
     }
   };
@@ -1167,17 +1161,8 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* C, int64_t ldc, i
 // Host side
 // ---------------------------------------------------------------------------
 
-thread_local std::string t_last_error;
-
-int set_error(int code, const char* fmt, ...) {
-  char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof buf, fmt, ap);
-  va_end(ap);
-  t_last_error = buf;
-  return code;
-}
+using hcg::set_error;
+using hcg::t_last_error;
 
 #define HCG_HIP_CHECK(expr)                                                               \
   do {                                                                                    \

@@ -262,6 +262,9 @@ def _gemm_torch(torch: Any, a: Any, b: Any, out: Any | None, algo: int) -> Any:
     return out
 
 
+from .tiles import tile_load, tile_store  # noqa: E402  (masked tile gather / scatter)
+
+
 def library_path() -> str:
     return _native.LIB_PATH
 
@@ -281,4 +284,6 @@ __all__ = [
     "library_path",
     "register_kernel",
     "run",
+    "tile_load",
+    "tile_store",
 ]

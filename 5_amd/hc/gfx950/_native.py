@@ -47,8 +47,9 @@ ALGOS = {
     "tiled_128x128": HCG_ALGO_TILED_128x128,
 }
 
-# Every symbol include/hcg_gemm.h declares.
-EXPORTS = ("hcg_init", "hcg_gemm", "hcg_gemm_algo", "hcg_last_error", "hcg_version")
+# Every symbol include/hcg_gemm.h and include/hcg_tile_ops.h declare.
+EXPORTS = ("hcg_init", "hcg_gemm", "hcg_gemm_algo", "hcg_last_error", "hcg_version", "hcg_tile_load",
+           "hcg_tile_store")
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -68,6 +69,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.hcg_last_error.restype = ctypes.c_char_p
     lib.hcg_version.argtypes = []
     lib.hcg_version.restype = c_int
+    u64 = ctypes.c_uint64
+    lib.hcg_tile_load.argtypes = [c_int, vp, i64, i64, i64, vp, i64, i64, i64, vp, u64, vp, vp, vp]
+    lib.hcg_tile_load.restype = c_int
+    lib.hcg_tile_store.argtypes = [c_int, vp, i64, i64, i64, vp, i64, i64, i64, vp, vp, vp]
+    lib.hcg_tile_store.restype = c_int
 
 
 def load() -> ctypes.CDLL:
@@ -124,3 +130,19 @@ def gemm(
     lib = load()
     rc = lib.hcg_gemm_algo(algo, dtype, a_ptr, lda, b_ptr, ldb, c_ptr, ldc, m, n, k, stream or None)
     check(lib, rc, "hcg_gemm")
+
+
+def tile_load(elem_bytes: int, src: int, ld: int, rows: int, cols: int, origins: int, ntiles: int, th: int,
+              tw: int, in_mask: int, fill_bits: int, out: int, out_mask: int, stream: int) -> None:
+    lib = load()
+    rc = lib.hcg_tile_load(elem_bytes, src or None, ld, rows, cols, origins or None, ntiles, th, tw,
+                           in_mask or None, fill_bits, out or None, out_mask or None, stream or None)
+    check(lib, rc, "hcg_tile_load")
+
+
+def tile_store(elem_bytes: int, dst: int, ld: int, rows: int, cols: int, origins: int, ntiles: int, th: int,
+               tw: int, tiles: int, tile_mask: int, stream: int) -> None:
+    lib = load()
+    rc = lib.hcg_tile_store(elem_bytes, dst or None, ld, rows, cols, origins or None, ntiles, th, tw,
+                            tiles or None, tile_mask or None, stream or None)
+    check(lib, rc, "hcg_tile_store")

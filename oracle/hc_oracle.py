@@ -31,6 +31,10 @@ Parity pins for each function live in tests/test_oracle.py:
   errors (a dropped k term, a transposed operand) that must fail.
 * :func:`simulate_lane_structure` -- bit-exact against the scalar triple loop
   (used only to time the reference's CPU path shape).
+* :func:`tile_load` / :func:`tile_store` (the masked tile access of
+  hc/simulator.py:1304-1357, 1416-1458) -- against per-element brute-force
+  loops, against plain numpy slices for interior tiles, and on hand-computed
+  edge, fully-outside and masked cases.
 """
 
 from __future__ import annotations
@@ -313,3 +317,57 @@ def parity_check(got: np.ndarray, want: np.ndarray, k: int, rel_fro_bound: float
     mx = float(np.max(np.abs(diff))) if diff.size else 0.0
     bound = max_abs_bound(k)
     return ParityReport(rel, mx, bound, rel_fro_bound, rel <= rel_fro_bound and mx <= bound)
+
+
+# --------------------------------------------------------------------------
+# Masked tile access (group.load / with_inactive / .mask / group.store)
+# --------------------------------------------------------------------------
+
+
+def tile_load(
+    src: np.ndarray, origins: np.ndarray, shape: tuple[int, int], mask: np.ndarray | None = None, fill=0
+) -> tuple[np.ndarray, np.ndarray]:
+    """Per tile t at origin (r0, c0): ``group.load(src[r0:r0+th, c0:c0+tw],
+    shape=(th, tw))`` -- the in-bounds overlap is copied, the rest is
+    inactive (``_copy_loaded_value``, hc/simulator.py:1338-1357) -- or with
+    ``mask``, active only where the mask is also true (``_load_masked``,
+    :1324-1336); then ``with_inactive(fill)`` and ``.mask``
+    (doc/langref.md:577-595).  Negative origins count as outside (the
+    slice is clipped to the part inside ``src``).  Returns (tiles, active)."""
+    th, tw = shape
+    origins = np.asarray(origins, dtype=np.int64).reshape(-1, 2)
+    n = origins.shape[0]
+    out = np.full((n, th, tw), fill, dtype=src.dtype)
+    active = np.zeros((n, th, tw), dtype=bool)
+    rows, cols = src.shape
+    for t, (r0, c0) in enumerate(origins):
+        # Tile rows/columns that fall inside src.
+        ra, rb = max(0, -r0), min(th, rows - r0)
+        ca, cb = max(0, -c0), min(tw, cols - c0)
+        if ra >= rb or ca >= cb:
+            continue
+        out[t, ra:rb, ca:cb] = src[r0 + ra : r0 + rb, c0 + ca : c0 + cb]
+        active[t, ra:rb, ca:cb] = True
+    if mask is not None:
+        active &= np.asarray(mask, dtype=bool)
+        out = np.where(active, out, np.array(fill, dtype=src.dtype))
+    return out, active
+
+
+def tile_store(dst: np.ndarray, origins: np.ndarray, tiles: np.ndarray, mask: np.ndarray | None = None) -> None:
+    """Per tile t at origin (r0, c0), in tile order: ``group.store(dst[r0:r0+th,
+    c0:c0+tw], tile)`` -- within the overlap of the view and the tile, active
+    elements are written and nothing else changes (``_store_from_value``,
+    hc/simulator.py:1441-1458).  Updates ``dst`` in place."""
+    n, th, tw = tiles.shape
+    origins = np.asarray(origins, dtype=np.int64).reshape(-1, 2)
+    act = np.ones(tiles.shape, dtype=bool) if mask is None else np.asarray(mask, dtype=bool)
+    rows, cols = dst.shape
+    for t, (r0, c0) in enumerate(origins):
+        ra, rb = max(0, -r0), min(th, rows - r0)
+        ca, cb = max(0, -c0), min(tw, cols - c0)
+        if ra >= rb or ca >= cb:
+            continue
+        region = dst[r0 + ra : r0 + rb, c0 + ca : c0 + cb]
+        sel = act[t, ra:rb, ca:cb]
+        region[sel] = tiles[t, ra:rb, ca:cb][sel]

@@ -1,6 +1,6 @@
 """The C ABI library: it is built, loads, exports every entry point that
-include/hcg_gemm.h declares, and rejects bad arguments on the host before
-any HIP call (no GPU needed for these)."""
+include/hcg_gemm.h and include/hcg_tile_ops.h declare, and rejects bad
+arguments on the host before any HIP call (no GPU needed for these)."""
 
 from __future__ import annotations
 
@@ -13,11 +13,11 @@ import pytest
 from hc.gfx950 import _native
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "hcg_gemm.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("hcg_gemm.h", "hcg_tile_ops.h")]
 
 
 def declared_functions() -> list[str]:
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(hcg_\w+)\s*\(", text, re.M)))
 
 
@@ -59,3 +59,30 @@ def test_empty_output_is_a_noop_and_clears_the_error():
     assert _native.last_error(lib)
     assert lib.hcg_gemm(0, None, 0, None, 0, None, 0, 0, 5, 5, None) == _native.HCG_OK
     assert _native.last_error(lib) == ""
+
+
+@pytest.mark.parametrize(
+    "args,match",
+    [
+        ((3, 0x1000, 4, 4, 4, 0x1000, 1, 2, 2, None, 0, 0x1000, None, None), "elem_bytes must be 2, 4 or 8"),
+        ((2, 0x1000, 4, -1, 4, 0x1000, 1, 2, 2, None, 0, 0x1000, None, None), "negative extent"),
+        ((2, None, 4, 4, 4, 0x1000, 1, 2, 2, None, 0, 0x1000, None, None), "view pointer is NULL"),
+        ((2, 0x1000, 3, 4, 4, 0x1000, 1, 2, 2, None, 0, 0x1000, None, None), r"ld \(3\) < cols \(4\)"),
+        ((2, 0x1000, 4, 4, 4, None, 1, 2, 2, None, 0, 0x1000, None, None), "origins is NULL"),
+        ((2, 0x1000, 4, 4, 4, 0x1000, 1, 2, 2, None, 0, None, None, None), "out is NULL"),
+    ],
+)
+def test_tile_load_rejects_bad_arguments_on_the_host(args, match):
+    lib = _native.load()
+    assert lib.hcg_tile_load(*args) == _native.HCG_EINVAL
+    assert re.search(match, _native.last_error(lib))
+
+
+def test_tile_ops_with_nothing_to_do_launch_nothing():
+    lib = _native.load()
+    # no tiles, empty tiles, and a store into an empty view
+    assert lib.hcg_tile_load(2, 0x1000, 4, 4, 4, None, 0, 2, 2, None, 0, None, None, None) == _native.HCG_OK
+    assert lib.hcg_tile_load(4, 0x1000, 4, 4, 4, 0x1000, 3, 0, 5, None, 0, None, None, None) == _native.HCG_OK
+    assert lib.hcg_tile_store(8, None, 0, 0, 0, 0x1000, 2, 2, 2, 0x1000, None, None) == _native.HCG_OK
+    assert lib.hcg_tile_store(2, 0x1000, 4, 4, 4, 0x1000, 1, 2, 2, None, None, None) == _native.HCG_EINVAL
+    assert "tiles is NULL" in _native.last_error(lib)

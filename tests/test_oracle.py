@@ -243,3 +243,97 @@ def test_lane_structured_simulation_is_the_same_fold(m, n, k):
     a, b = make_demo_inputs(m=m, n=n, k=k, seed=5)
     got = oracle.simulate_lane_structure(a, b)
     assert np.array_equal(got.view(np.uint32), oracle.gemm_bruteforce(a, b).view(np.uint32))
+
+
+# -- masked tile access (hc/simulator.py:1304-1357, 1416-1458) ---------------------
+
+
+def _tile_load_elementwise(src, origins, shape, mask, fill):
+    """Per-element restatement: element (t, r, c) is active iff its source
+    coordinate lies inside src (and the mask allows it)."""
+    th, tw = shape
+    n = len(origins)
+    out = np.full((n, th, tw), fill, dtype=src.dtype)
+    act = np.zeros((n, th, tw), dtype=bool)
+    for t, (r0, c0) in enumerate(origins):
+        for r in range(th):
+            for c in range(tw):
+                i, j = r0 + r, c0 + c
+                if 0 <= i < src.shape[0] and 0 <= j < src.shape[1] and (mask is None or mask[t, r, c]):
+                    out[t, r, c] = src[i, j]
+                    act[t, r, c] = True
+    return out, act
+
+
+def _copy_loaded_value_reference_form(src, r0, c0, th, tw):
+    """The reference's own formulation for non-negative origins: slice the
+    source (numpy clips at the edges), copy the overlap into a zero tile,
+    mark it active (hc/simulator.py:1338-1357)."""
+    view = src[r0 : r0 + th, c0 : c0 + tw]
+    data = np.zeros((th, tw), dtype=src.dtype)
+    act = np.zeros((th, tw), dtype=bool)
+    data[: view.shape[0], : view.shape[1]] = view
+    act[: view.shape[0], : view.shape[1]] = True
+    return data, act
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.float32, np.int64])
+def test_tile_load_oracle_matches_elementwise_and_reference_slicing(dtype):
+    rng = np.random.default_rng(5)
+    src = rng.integers(-1000, 1000, size=(23, 31)).astype(dtype)
+    origins = np.array([[0, 0], [7, 9], [20, 28], [22, 30], [23, 0], [0, 31], [-3, -2], [-1, 25], [40, 40]])
+    mask = rng.random((len(origins), 5, 6)) < 0.7
+    for m in (None, mask):
+        got, act = oracle.tile_load(src, origins, (5, 6), mask=m, fill=7)
+        want, wact = _tile_load_elementwise(src, origins, (5, 6), m, 7)
+        assert np.array_equal(got, want) and np.array_equal(act, wact)
+    got, act = oracle.tile_load(src, origins, (5, 6), fill=0)
+    for t, (r0, c0) in enumerate(origins):
+        if r0 >= 0 and c0 >= 0:
+            d, a = _copy_loaded_value_reference_form(src, r0, c0, 5, 6)
+            assert np.array_equal(got[t], d) and np.array_equal(act[t], a)
+
+
+def test_tile_load_oracle_known_answers():
+    src = np.arange(20, dtype=np.float32).reshape(4, 5)
+    got, act = oracle.tile_load(src, [[2, 3], [-1, -1], [10, 0], [1, 1]], (3, 3), fill=-1)
+    assert got[0].tolist() == [[13, 14, -1], [18, 19, -1], [-1, -1, -1]]
+    assert act[0].sum() == 4
+    assert got[1].tolist() == [[-1, -1, -1], [-1, 0, 1], [-1, 5, 6]]
+    assert not act[2].any() and np.all(got[2] == -1)
+    assert np.array_equal(got[3], src[1:4, 1:4]) and act[3].all()  # interior tile = plain slice
+    # with_inactive keeps active payloads, replaces inactive ones (doc/langref.md:577-580)
+    m = np.zeros((4, 3, 3), dtype=bool)
+    m[3, 1, 1] = True
+    got, act = oracle.tile_load(src, [[2, 3], [-1, -1], [10, 0], [1, 1]], (3, 3), mask=m, fill=9)
+    assert act.sum() == 1 and got[3, 1, 1] == src[2, 2] and np.sum(got == 9) == 4 * 9 - 1
+
+
+def test_tile_store_oracle_matches_elementwise_and_leaves_the_rest():
+    rng = np.random.default_rng(6)
+    origins = np.array([[0, 0], [5, 11], [18, 27], [-2, 3], [30, 30], [10, -4]])
+    tiles = rng.integers(1, 100, size=(len(origins), 6, 7)).astype(np.float32)
+    mask = rng.random(tiles.shape) < 0.6
+    for m in (None, mask):
+        dst = np.full((21, 30), np.nan, dtype=np.float32)
+        oracle.tile_store(dst, origins, tiles, mask=m)
+        want = np.full((21, 30), np.nan, dtype=np.float32)
+        for t, (r0, c0) in enumerate(origins):
+            for r in range(6):
+                for c in range(7):
+                    i, j = r0 + r, c0 + c
+                    if 0 <= i < 21 and 0 <= j < 30 and (m is None or m[t, r, c]):
+                        want[i, j] = tiles[t, r, c]
+        assert np.array_equal(np.isnan(dst), np.isnan(want))
+        assert np.array_equal(dst[~np.isnan(dst)], want[~np.isnan(want)])
+
+
+def test_tile_store_then_load_round_trips_inside_the_view():
+    rng = np.random.default_rng(7)
+    dst = np.zeros((17, 19), dtype=np.float16)
+    origins = np.array([[0, 0], [8, 10], [12, 14]])
+    tiles = rng.standard_normal((3, 8, 10)).astype(np.float16)
+    oracle.tile_store(dst, origins[:2], tiles[:2])
+    back, act = oracle.tile_load(dst, origins[:2], (8, 10))
+    assert np.array_equal(back[act], tiles[:2][act])
+    assert act[0].all() and act[1].sum() == min(8, 17 - 8) * min(10, 19 - 10)
