@@ -686,33 +686,53 @@ struct RepackJob {
   int64_t chunks;  // rows * ld_out / 8
 };
 
-// Each thread writes four 8-element output chunks, 256 chunks apart; the
-// source words of all four are gathered before any is shifted and stored,
-// so that the thread has their loads in flight at once.  A chunk that lies
-// inside its row is read as aligned 4-byte words: 4 words when its first
-// element starts a word, else 5 words and a 16-bit funnel shift.  The first
-// and last words read each hold an element of the chunk, so no read leaves
-// the words that hold valid data.  The row's final, partial chunk is read
-// element by element.
-constexpr int kRepackPer = 4;
+// Bytes [o, o + 16) of the 32 bytes w0:w1 (o even, 0 .. 14): a word rotate
+// by o / 4 (two selects, on named registers so that no register array is
+// indexed dynamically) and a byte funnel shift by o % 4.
+__device__ __forceinline__ u32x4 shift_join(u32x4 w0, u32x4 w1, int o) {
+  const uint32_t a0 = w0[0], a1 = w0[1], a2 = w0[2], a3 = w0[3], a4 = w1[0], a5 = w1[1], a6 = w1[2], a7 = w1[3];
+  const bool s1 = (o >> 2) & 1, s2 = (o >> 3) & 1;
+  const uint32_t b0 = s2 ? a2 : a0, b1 = s2 ? a3 : a1, b2 = s2 ? a4 : a2, b3 = s2 ? a5 : a3, b4 = s2 ? a6 : a4,
+                 b5 = s2 ? a7 : a5;
+  const uint32_t c0 = s1 ? b1 : b0, c1 = s1 ? b2 : b1, c2 = s1 ? b3 : b2, c3 = s1 ? b4 : b3, c4 = s1 ? b5 : b4;
+  const int bs = o & 3;
+  return u32x4{__builtin_amdgcn_alignbyte(c1, c0, bs), __builtin_amdgcn_alignbyte(c2, c1, bs),
+               __builtin_amdgcn_alignbyte(c3, c2, bs), __builtin_amdgcn_alignbyte(c4, c3, bs)};
+}
 
+// Output chunks (8 elements, 16 bytes) per thread, gridDim.x * 256 apart;
+// all their loads are issued before any is shifted and stored.
+constexpr int kRepackPer = 2;
+
+// Each output chunk's source bytes are addressed from the 16-byte boundary
+// at or below src ("aligned bytes"): the chunk starts at aligned byte
+// 2f + pre (f = flat element index, pre = src's offset in its 16-byte
+// block) and lies in aligned chunks q and q + 1, both read with aligned
+// 16-byte loads and joined by shift_join.  Chunk q + 1 is read only when it
+// holds a byte of the operand (a 16-byte chunk never crosses a page, so one
+// holding any valid byte can be read whole); elements past the row's
+// `cols` are cleared after the join.
 __global__ __launch_bounds__(256) void repack_kernel(RepackJob a, RepackJob b) {
-  const int64_t base = (int64_t)blockIdx.x * (256 * kRepackPer) + threadIdx.x;
-  uint32_t w[kRepackPer][5];
+  const int64_t n = a.chunks + b.chunks;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const int64_t first = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  u32x4 w0[kRepackPer], w1[kRepackPer];
+  int o[kRepackPer], valid[kRepackPer];
   uint16_t* dst[kRepackPer];
-  int mode[kRepackPer];  // 0: 4 aligned words, 1: 5 words + shift, 2: partial row end, 3: none
 #pragma unroll
   for (int i = 0; i < kRepackPer; ++i) {
-    int64_t idx = base + 256 * i;
+    int64_t idx = first + i * stride;
+    dst[i] = nullptr;
+    valid[i] = 0;
+    o[i] = 0;
+    w0[i] = u32x4{0, 0, 0, 0};
+    w1[i] = u32x4{0, 0, 0, 0};
+    if (idx >= n) continue;
     const bool in_a = idx < a.chunks;
     if (!in_a) idx -= a.chunks;
-    mode[i] = 3;
-    dst[i] = nullptr;
-#pragma unroll
-    for (int e = 0; e < 5; ++e) w[i][e] = 0;
-    if (!in_a && idx >= b.chunks) continue;
     const uint16_t* src = in_a ? a.src : b.src;
     const int64_t ld = in_a ? a.ld : b.ld;
+    const int rows = in_a ? a.rows : b.rows;
     const int cols = in_a ? a.cols : b.cols;
     const int ld_out = in_a ? a.ld_out : b.ld_out;
     // chunks < 2^27 (a repacked operand stays below 2^31 bytes), so 32-bit
@@ -720,37 +740,32 @@ __global__ __launch_bounds__(256) void repack_kernel(RepackJob a, RepackJob b) {
     const uint32_t per_row = (uint32_t)ld_out / 8;
     const int row = (int)((uint32_t)idx / per_row);
     const int c0 = (int)((uint32_t)idx - (uint32_t)row * per_row) * 8;
-    const int64_t f = (int64_t)row * ld + c0;  // flat source element index
     dst[i] = (in_a ? a.dst : b.dst) + (int64_t)row * ld_out + c0;
-    if (c0 + 8 <= cols) {
-      // Element index counted from the 4-byte boundary at or below src.
-      const int off = (int)((reinterpret_cast<uintptr_t>(src) >> 1) & 1);
-      const int64_t g = f + off;
-      const uint32_t* q =
-          reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(src) - 2 * off) + (g >> 1);
-      mode[i] = (int)(g & 1);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) w[i][e] = q[e];
-      if (mode[i]) w[i][4] = q[4];
-    } else {
-      mode[i] = 2;
-      const uint16_t* p = src + f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int c = c0 + 2 * e;
-        const uint32_t lo = c < cols ? p[2 * e] : 0u;
-        const uint32_t hi = c + 1 < cols ? p[2 * e + 1] : 0u;
-        w[i][e] = lo | (hi << 16);
-      }
-    }
+    valid[i] = cols - c0;
+    if (c0 >= cols) continue;
+    const uintptr_t base = reinterpret_cast<uintptr_t>(src) & ~(uintptr_t)15;
+    const int pre = (int)(reinterpret_cast<uintptr_t>(src) & 15);
+    const int64_t start = ((int64_t)row * ld + c0) * 2 + pre;
+    const int64_t last = (((int64_t)rows - 1) * ld + cols) * 2 - 1 + pre;
+    const int64_t q = start >> 4;
+    o[i] = (int)(start & 15);
+    const u32x4* p = reinterpret_cast<const u32x4*>(base) + q;
+    w0[i] = p[0];
+    if (o[i] != 0 && (q + 1) * 16 <= last) w1[i] = p[1];
   }
 #pragma unroll
   for (int i = 0; i < kRepackPer; ++i) {
-    if (mode[i] == 3) continue;
-    u32x4 out{w[i][0], w[i][1], w[i][2], w[i][3]};
-    if (mode[i] == 1) {
+    if (dst[i] == nullptr) continue;
+    u32x4 out = u32x4{0, 0, 0, 0};
+    if (valid[i] > 0) {
+      out = shift_join(w0[i], w1[i], o[i]);
+      if (valid[i] < 8) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) out[e] = (w[i][e] >> 16) | (w[i][e + 1] << 16);
+        for (int k = 0; k < 4; ++k) {
+          if (2 * k >= valid[i]) out[k] = 0;
+          else if (2 * k + 1 >= valid[i]) out[k] &= 0xffffu;
+        }
+      }
     }
     *reinterpret_cast<u32x4*>(dst[i]) = out;
   }
@@ -1529,7 +1544,7 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
       b_use = b_p;
     }
     const int64_t n = ja.chunks + jb.chunks;
-    const int64_t per_block = 256 * kRepackPer;
+    const int64_t per_block = (int64_t)256 * kRepackPer;
     repack_kernel<<<(unsigned)((n + per_block - 1) / per_block), 256, 0, stream>>>(ja, jb);
     HCG_HIP_CHECK(hipGetLastError());
   }
