@@ -1,0 +1,106 @@
+"""Launches from several host threads, and HIP-graph capture and replay.
+
+The reference runs concurrent launches from two threads
+(tests/test_simulator.py:1113-1125); here each thread drives its own stream
+through the C ABI.  Graph capture: the kernels take no host-side action
+inside a launch except on a stream's first use of a workspace size (an
+allocation), so after one warm-up call on the capture stream every path --
+tiled, skinny split-K (workspace partials + reduce) and repacked ragged
+operands (workspace copies) -- records into a graph.  Every replay is
+checked against the eager result, with eager work between replays.
+"""
+
+from __future__ import annotations
+
+import threading
+
+import numpy as np
+import pytest
+
+import hc_oracle as oracle
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+DEV = "cuda:0"
+
+
+def _dev(x, dtype="float16"):
+    from hc.gfx950.workloads import to_torch
+
+    return to_torch(x, dtype, torch.device(DEV))
+
+
+CASES = [
+    ("tiled", 1024, 768, 512),
+    ("skinny", 16, 4096, 4096),
+    ("ragged", 1000, 601, 333),
+]
+
+
+def _inputs(name, m, n, k, seed):
+    from hc.gfx950.workloads import make_inputs
+
+    return make_inputs("c4_skinny_f16" if name == "skinny" else "c2_4096_f16", seed=seed, m=m, n=n, k=k)
+
+
+def test_two_host_threads_each_with_a_stream():
+    import hc.gfx950 as g
+
+    jobs = []
+    for i, (name, m, n, k) in enumerate(CASES * 2):
+        a, b = _inputs(name, m, n, k, seed=100 + i)
+        jobs.append((a, b, _dev(a), _dev(b), torch.empty((m, n), dtype=torch.float32, device=DEV)))
+    errors = []
+    barrier = threading.Barrier(2)
+
+    def worker(part):
+        try:
+            s = torch.cuda.Stream(device=DEV)
+            barrier.wait()
+            with torch.cuda.stream(s):
+                for _ in range(5):
+                    for _, _, ta, tb, tc in part:
+                        g.gemm(ta, tb, out=tc)
+            s.synchronize()
+        except Exception as exc:  # surfaced below
+            errors.append(exc)
+
+    threads = [threading.Thread(target=worker, args=(jobs[i::2],)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not errors, errors
+    for a, b, _, _, tc in jobs:
+        rep = oracle.parity_check(tc.cpu().numpy(), oracle.gemm_c(a, b), a.shape[1])
+        assert rep.ok, str(rep)
+
+
+@pytest.mark.parametrize("name,m,n,k", CASES)
+def test_graph_capture_replays_match_eager(name, m, n, k):
+    import hc.gfx950 as g
+
+    a, b = _inputs(name, m, n, k, seed=7)
+    ta, tb = _dev(a), _dev(b)
+    out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    s = torch.cuda.Stream(device=DEV)
+    with torch.cuda.stream(s):
+        g.gemm(ta, tb, out=out)  # warm-up: allocates this stream's workspace if the path needs one
+    s.synchronize()
+    eager = out.clone()
+    rep = oracle.parity_check(eager.cpu().numpy(), oracle.gemm_c(a, b), k)
+    assert rep.ok, str(rep)
+    print(f"case graph {name} m={m} n={n} k={k}", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        g.gemm(ta, tb, out=out)
+    for i in range(4):
+        out.fill_(float("nan"))
+        # eager work on the same stream between replays
+        with torch.cuda.stream(s):
+            g.gemm(ta, tb, out=torch.empty_like(out))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
