@@ -9,19 +9,26 @@
 // 64-wide wavefronts and the v_mfma_f32_{32x32x16,16x16x32}_{f16,bf16}
 // matrix cores:
 //
-//   * gemm_dma_kernel -- compute-bound shapes.  256x256 output tile per
-//     256-thread workgroup (4 waves in 2x2, each 128x128 = 4x4 MFMA 32x32x16
-//     tiles), K step 32 through a 4-stage LDS ring filled by direct
-//     global->LDS DMA loads (buffer_load ... lds), B kept row-major in LDS
-//     and read with transposing LDS loads (ds_read_b64_tr_b16), XOR-swizzled
+//   * gemm_dma_kernel -- compute-bound shapes.  TM x TN output tile per
+//     256-thread workgroup (256x256, 256x192, 128x256 or 128x128, picked by
+//     size; 4 waves in 2x2, each (TM/2) x (TN/2) of MFMA 32x32x16 tiles),
+//     K step 32 through an LDS ring filled by direct global->LDS DMA loads
+//     (buffer_load ... lds), B kept row-major in LDS and read with
+//     transposing LDS loads (ds_read_b64_tr_b16), XOR-swizzled
 //     bank-conflict-free layouts, XCD-aware tile order, masked M/N/K tails
 //     by the buffer range check, and an LDS-staged 16-byte epilogue.
+//   * gemm_stream_kernel -- M <= 16 with aligned operands (HBM-bound).  B
+//     streams HBM -> LDS once through a DMA ring, split over K across
+//     workgroups mapped so every XCD covers all column residues; the split
+//     partials are summed in a fixed order (deterministic).
 //   * gemm_generic_kernel -- fallback for operands whose byte offsets do not
 //     fit 31 bits: plain pointers, register staging, any alignment.
-//   * gemm_skinny_kernel -- M <= 16 (HBM-bound).  One 16-row MFMA 16x16x32
-//     block covers all of A; B is streamed exactly once with 128-bit loads,
-//     transposed 8x8 in registers, split over K across waves and workgroups;
-//     partial sums are reduced in a fixed order (deterministic).
+//   * gemm_skinny_kernel -- M <= 16 with unaligned operands: B streamed with
+//     128-bit loads, transposed 8x8 in registers, split over K; partial sums
+//     reduced in a fixed order.
+//   * repack_kernel -- copies operands whose rows are not 16-byte aligned
+//     (or whose K / N is not a multiple of 8) into zero-padded aligned rows
+//     for the DMA kernels.
 //
 // Numerics: products of fp16/bf16 values are exact in float32 and the MFMA
 // accumulates in float32; only the order of the float32 additions differs
@@ -297,15 +304,16 @@ constexpr int kSgDsRead = 0x100;
 // DMA tiled kernel: global -> LDS with buffer_load ... lds (no VGPR staging)
 // ---------------------------------------------------------------------------
 //
-// TM x 256 output tile (TM = 256 or 128), 4 waves (2x2, each TM/2 x 128 =
-// TM/64 x 4 MFMA 32x32x16 tiles), K step 32, and a STAGES-deep LDS ring:
-// tile kt+STAGES-1 is requested while tile kt is multiplied.  TM = 256 uses
-// 4 stages (128 KB, one workgroup per CU); TM = 128 uses 3 stages (72 KB) so
-// two workgroups share a CU -- for shapes with too few 256x256 tiles to fill
-// the chip.
+// TM x TN output tile, 4 waves (2x2, each TM/2 x TN/2 = TM/64 x TN/64 MFMA
+// 32x32x16 tiles), K step 32, and a STAGES-deep LDS ring:
+// a stage is refilled (tile kt + STAGES) as soon as the barrier after its
+// last fragment reads has passed.  TM = 256 uses 4 stages (128 KB, one
+// workgroup per CU); TM = 128 uses 3 stages (72 KB) so two workgroups share
+// a CU -- for shapes with too few large tiles to fill the chip.
 //
 // Stage layout: A as [TM rows][32 k] (64-byte rows of 4 chunks of 16 bytes),
-// B as [32 k][256 n] (512-byte rows of 32 chunks); chunks are XOR-swizzled
+// B as [32 k][256 n] (512-byte rows of 32 chunks, whatever TN; chunks past
+// TN are zero-filled and never read); chunks are XOR-swizzled
 // per row (a_chunk_swz, b_chunk_swz).  A fragments are one ds_read_b128; B
 // fragments are two ds_read_b64_tr_b16, which within each 16-lane group
 // hand lane i element i%4 of source lane 4j + i/4 (j = 0..3): source lanes
