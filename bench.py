@@ -150,7 +150,28 @@ def cpu_baseline(cfg, a, b, target_s: float) -> dict:
         "kind": "port",
         "sample": f"rows 0..{rows - 1} of {cfg.name} ({rows}x{cfg.n}x{cfg.k}) x {reps}, {elapsed:.1f} s, "
         f"C oracle (sequential fp32 fold, OpenMP over row blocks) on {os.cpu_count()} host CPUs",
+        "single_thread": single_thread_baseline(cfg, a, b, dt),
         "simulator_shape": simulator_shape_baseline(cfg),
+    }
+
+
+def single_thread_baseline(cfg, a, b, dt) -> dict:
+    """The same C oracle on one host thread, over a fixed sample of 256 rows
+    (about 2 s on these hosts)."""
+    import numpy as np
+
+    import hc_oracle
+
+    rows = min(cfg.m, 256)
+    idx = np.arange(rows, dtype=np.int64)
+    t0 = time.perf_counter()
+    hc_oracle.gemm_c_rows(a, b, idx, dt, threads=1)
+    elapsed = time.perf_counter() - t0
+    return {
+        "value": 2.0 * rows * cfg.n * cfg.k / elapsed / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "sample": f"rows 0..{rows - 1} of {cfg.name} ({rows}x{cfg.n}x{cfg.k}), {elapsed:.2f} s",
     }
 
 
