@@ -199,3 +199,54 @@ def test_gemm_entry_validates_before_touching_a_device():
         g.gemm(np.zeros((2, 3), np.float16), np.zeros((3, 2), np.float16), algo="fast")
     with pytest.raises(LaunchError, match="C shape"):
         g.gemm(np.zeros((2, 3), np.float16), np.zeros((3, 2), np.float16), out=np.zeros((3, 3), np.float32))
+
+
+def test_gfx950_intrinsic_fallback_body_is_one_mfma_step():
+    """Run the wave64 intrinsic's fallback body for all 64 lanes (stand-in
+    tile and group objects) and assemble the 32x32 result from the stated
+    lane layout: it must equal acc + A @ B as the oracle's sequential float32
+    fold, with masked-off (inactive) operand entries counting as +0."""
+    import hc_oracle as oracle
+    from hc.gfx950 import kernels
+
+    class Tile:
+        def __init__(self, data, active):
+            self.data, self.active = data, active
+
+        def with_inactive(self, value):
+            return np.where(self.active, self.data, np.asarray(value, dtype=self.data.dtype))
+
+    class Group:
+        @staticmethod
+        def vload(values, shape):
+            assert tuple(shape) == (kernels.ACC_REGS,)
+            return np.asarray(values, dtype=np.float32)
+
+    rng = np.random.default_rng(4)
+    a = rng.uniform(-1, 1, (32, 16)).astype(np.float16)
+    b = rng.uniform(-1, 1, (16, 32)).astype(np.float16)
+    a_act = rng.random(a.shape) < 0.9
+    b_act = rng.random(b.shape) < 0.9
+    a0 = np.where(a_act, a, np.float16(0))
+    b0 = np.where(b_act, b, np.float16(0))
+
+    def run(acc0):
+        out = np.full((32, 32), np.nan, dtype=np.float32)
+        for lane in range(64):
+            rows = kernels.lane_acc_rows(lane)
+            col = kernels.lane_column(lane)
+            frag = np.array([acc0[r, col] for r in rows], dtype=np.float32)
+            res = kernels.mfma_gfx950(Group, Tile(a, a_act), Tile(b, b_act), frag, lane=lane, wave_size=64,
+                                      arch="gfx950")
+            for reg, r in enumerate(rows):
+                out[r, col] = res[reg]
+        return out
+
+    # From zero accumulators: exactly the oracle's fold of the masked operands.
+    assert np.array_equal(run(np.zeros((32, 32), np.float32)), oracle.gemm_sequential(a0, b0))
+    # From nonzero accumulators: the fold continues from them, k ascending.
+    acc0 = rng.uniform(-4, 4, (32, 32)).astype(np.float32)
+    want = acc0.copy()
+    for k in range(16):
+        want = (want + a0[:, k : k + 1].astype(np.float32) * b0[k : k + 1, :].astype(np.float32)).astype(np.float32)
+    assert np.array_equal(run(acc0), want)
