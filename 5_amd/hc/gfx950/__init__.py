@@ -42,6 +42,7 @@ TARGET_NAME = "amdgpu-gfx950"
 KNOWN_GEMM_KERNELS = frozenset({"tiled_gfx11_wmma_matmul", "tiled_gfx950_mfma_matmul"})
 
 _DTYPE_CODES = {"float16": _native.HCG_F16, "bfloat16": _native.HCG_BF16}
+_TORCH_DTYPE_CODES: dict[Any, int] = {}
 
 
 @dataclass(frozen=True)
@@ -156,11 +157,6 @@ def _torch():
     return torch
 
 
-def _row_stride(t: Any) -> int:
-    rows, cols = int(t.shape[0]), int(t.shape[1])
-    return int(t.stride(0)) if rows > 1 else max(cols, 1)
-
-
 def _check_shapes(a: Any, b: Any, c: Any | None) -> tuple[int, int, int]:
     if len(a.shape) != 2 or len(b.shape) != 2:
         raise LaunchError("A and B must be rank-2 matrices")
@@ -188,18 +184,16 @@ def gemm(a: Any, b: Any, out: Any | None = None, *, algo: str = "auto", device: 
     computed, and copied back into ``out`` (created if None); the call then
     returns after the result is on the host.
     """
-    if algo not in _native.ALGOS:
+    algo_code = _native.ALGOS.get(algo)
+    if algo_code is None:
         raise LaunchError(f"unknown algo {algo!r}; expected one of {sorted(_native.ALGOS)}")
-    algo_code = _native.ALGOS[algo]
     torch_mod = _torch()
-    is_np = [isinstance(x, np.ndarray) for x in (a, b)]
-    if all(is_np) and (out is None or isinstance(out, np.ndarray)):
+    tensor = torch_mod.Tensor
+    if isinstance(a, tensor) and isinstance(b, tensor) and (out is None or isinstance(out, tensor)):
+        return _gemm_torch(torch_mod, a, b, out, algo_code)
+    if isinstance(a, np.ndarray) and isinstance(b, np.ndarray) and (out is None or isinstance(out, np.ndarray)):
         return _gemm_numpy(torch_mod, a, b, out, algo_code, device)
-    if not all(isinstance(x, torch_mod.Tensor) for x in (a, b)) or (
-        out is not None and not isinstance(out, torch_mod.Tensor)
-    ):
-        raise LaunchError("A, B and C must all be numpy arrays or all be torch tensors")
-    return _gemm_torch(torch_mod, a, b, out, algo_code)
+    raise LaunchError("A, B and C must all be numpy arrays or all be torch tensors")
 
 
 def _gemm_numpy(torch: Any, a: np.ndarray, b: np.ndarray, out: np.ndarray | None, algo: int, device: int | None) -> np.ndarray:
@@ -222,41 +216,64 @@ def _gemm_numpy(torch: Any, a: np.ndarray, b: np.ndarray, out: np.ndarray | None
     return out
 
 
+def _torch_dtype_code(torch: Any, a: Any, b: Any) -> int:
+    if not _TORCH_DTYPE_CODES:
+        _TORCH_DTYPE_CODES.update({torch.float16: _native.HCG_F16, torch.bfloat16: _native.HCG_BF16})
+    code = _TORCH_DTYPE_CODES.get(a.dtype)
+    if code is None or b.dtype != a.dtype:
+        return _dtype_code(a, b)  # raises, naming both dtypes
+    return code
+
+
+def _current_stream(torch: Any, index: int) -> int:
+    """Raw handle of the current torch stream of device ``index``.
+
+    ``torch._C._cuda_getCurrentRawStream`` returns it without building a
+    ``torch.cuda.Stream`` object (a few microseconds per call); the public
+    route is kept for a torch build that lacks it."""
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return raw(index)
+    return torch.cuda.current_stream(index).cuda_stream
+
+
 def _gemm_torch(torch: Any, a: Any, b: Any, out: Any | None, algo: int) -> Any:
     m, n, k = _check_shapes(a, b, out)
     if not (a.is_cuda and b.is_cuda) or (out is not None and not out.is_cuda):
         raise LaunchError("torch tensors must live on a GPU")
-    if b.device != a.device or (out is not None and out.device != a.device):
+    dev = a.device
+    if b.device != dev or (out is not None and out.device != dev):
         raise LaunchError("A, B and C must live on the same device")
-    dtype = _dtype_code(a, b)
+    dtype = _torch_dtype_code(torch, a, b)
     if out is None:
-        out = torch.empty((m, n), dtype=torch.float32, device=a.device)
+        out = torch.empty((m, n), dtype=torch.float32, device=dev)
     elif out.dtype != torch.float32:
         raise LaunchError(f"C dtype expected float32, got {str(out.dtype).replace('torch.', '')}")
     if m == 0 or n == 0:
         return out
-    if k > 0 and (a.stride(1) != 1 or (m > 1 and a.stride(0) < k)):
+    sa, sb, so = a.stride(), b.stride(), out.stride()
+    if k > 0 and (sa[1] != 1 or (m > 1 and sa[0] < k)):
         a = a.contiguous()
-    if k > 0 and (b.stride(1) != 1 or (k > 1 and b.stride(0) < n)):
+        sa = a.stride()
+    if k > 0 and (sb[1] != 1 or (k > 1 and sb[0] < n)):
         b = b.contiguous()
-    direct = (out.stride(1) == 1 or n == 1) and (m == 1 or out.stride(0) >= n)
-    target = out if direct else torch.empty((m, n), dtype=torch.float32, device=a.device)
-    with torch.cuda.device(a.device):
-        stream = torch.cuda.current_stream(a.device).cuda_stream
-        _native.gemm(
-            algo,
-            dtype,
-            a.data_ptr(),
-            max(_row_stride(a), k),
-            b.data_ptr(),
-            max(_row_stride(b), n),
-            target.data_ptr(),
-            max(_row_stride(target), n),
-            m,
-            n,
-            k,
-            stream,
-        )
+        sb = b.stride()
+    direct = (so[1] == 1 or n == 1) and (m == 1 or so[0] >= n)
+    target = out if direct else torch.empty((m, n), dtype=torch.float32, device=dev)
+    st = so if direct else target.stride()
+    # Row strides as the C ABI reads them: a one-row matrix's stride is
+    # unused, so report the smallest legal one.
+    lda = max(sa[0], k) if m > 1 else max(k, 1)
+    ldb = max(sb[0], n) if k > 1 else max(n, 1)
+    ldc = max(st[0], n) if m > 1 else max(n, 1)
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    if torch.cuda.current_device() == index:
+        _native.gemm(algo, dtype, a.data_ptr(), lda, b.data_ptr(), ldb, target.data_ptr(), ldc, m, n, k,
+                     _current_stream(torch, index))
+    else:
+        with torch.cuda.device(index):
+            _native.gemm(algo, dtype, a.data_ptr(), lda, b.data_ptr(), ldb, target.data_ptr(), ldc, m, n, k,
+                         _current_stream(torch, index))
     if target is not out:
         out.copy_(target)
     return out

@@ -127,7 +127,7 @@ def gemm(
     k: int,
     stream: int,
 ) -> None:
-    lib = load()
+    lib = _lib if _lib is not None else load()
     rc = lib.hcg_gemm_algo(algo, dtype, a_ptr, lda, b_ptr, ldb, c_ptr, ldc, m, n, k, stream or None)
     check(lib, rc, "hcg_gemm")
 
