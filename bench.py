@@ -19,7 +19,9 @@ metric configuration, fp16 M=N=K=4096; ``value`` is TFLOP/s
   bytes against the 8 TB/s HBM peak, timed while rotating through enough
   copies of B that every launch streams B from HBM, not from the 256 MB
   Infinity Cache (warm, same-buffer numbers are reported beside it);
-* ``others``: the remaining BASELINE.json configurations, TFLOP/s.
+* ``others``: the remaining BASELINE.json configurations, TFLOP/s;
+* ``board``: graphics (per XCD too) and memory clocks and socket power
+  sampled from the driver while the headline workload runs.
 """
 
 from __future__ import annotations
@@ -111,6 +113,109 @@ def time_launches(torch, stream, fn, steps: int, warmup: int) -> tuple[float, fl
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     return start.elapsed_time(end) * 1e-3 / steps, (t1 - t0) / steps
+
+
+def median_launch(torch, stream, fn, launches: int) -> float:
+    """Median seconds of single launches, each bracketed by its own pair of
+    HIP events (run after time_launches, so the clock has settled)."""
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(launches)]
+    with torch.cuda.stream(stream):
+        for start, end in pairs:
+            start.record(stream)
+            fn()
+            end.record(stream)
+    torch.cuda.synchronize()
+    times = sorted(start.elapsed_time(end) * 1e-3 for start, end in pairs)
+    return times[len(times) // 2]
+
+
+def _smi_handle(amdsmi, torch):
+    handles = amdsmi.amdsmi_get_processor_handles()
+    if len(handles) == 1:
+        return handles[0]
+    props = torch.cuda.get_device_properties(0)
+    for h in handles:
+        bdf = amdsmi.amdsmi_get_gpu_device_bdf(h)  # "dddd:bb:dd.f"
+        dom, bus, rest = bdf.split(":")
+        if int(dom, 16) == props.pci_domain_id and int(bus, 16) == props.pci_bus_id and int(rest.split(".")[0], 16) == props.pci_device_id:
+            return h
+    raise RuntimeError("no amdsmi handle matches cuda:0")
+
+
+def board_state(torch, stream, fn, seconds: float) -> dict:
+    """Clocks and power the driver reports while ``fn`` runs back to back.
+
+    The SMU refreshes the gpu_metrics table (read through amdsmi) about once
+    a second, so ``seconds`` of launches follow the timed region and a
+    thread reads the table every 20 ms; the values reported come from the
+    last refresh made at least 1.05 s into the load, whose averaging window
+    therefore lies under load.  ``current_gfxclk`` is the SMU's clock
+    setting: the effective shader clock under a power limit can be lower
+    (compare ``achieved`` with the MFMA rate).  Only reads are made.
+    Returns {"error": ...} where amdsmi is unavailable."""
+    import threading
+
+    try:
+        import amdsmi
+
+        amdsmi.amdsmi_init()
+    except Exception as exc:  # reported, never fatal
+        return {"error": f"amdsmi unavailable: {exc}"}
+    try:
+        handle = _smi_handle(amdsmi, torch)
+        samples: list[tuple[float, dict]] = []
+        errors: list[str] = []
+        stop = threading.Event()
+        t0 = time.perf_counter()
+
+        def sampler():
+            while not stop.is_set():
+                try:
+                    samples.append((time.perf_counter() - t0, amdsmi.amdsmi_get_gpu_metrics_info(handle)))
+                except Exception as exc:
+                    errors.append(str(exc))
+                    return
+                stop.wait(0.02)
+
+        t = threading.Thread(target=sampler, daemon=True)
+        t.start()
+        with torch.cuda.stream(stream):
+            while time.perf_counter() - t0 < seconds:
+                for _ in range(20):
+                    fn()
+                stream.synchronize()
+        stop.set()
+        t.join(timeout=5)
+        if not samples:
+            return {"error": errors[0] if errors else "no gpu_metrics sample"}
+        first_ts = samples[0][1].get("firmware_timestamp")
+        under_load = [m for ts, m in samples if ts >= 1.05 and m.get("firmware_timestamp") != first_ts]
+        pick = under_load[-1] if under_load else samples[-1][1]
+
+        def num(x):
+            return x if isinstance(x, (int, float)) and not isinstance(x, bool) and x < 0xFFFF else None
+
+        xcd = pick.get("current_gfxclks")
+        out = {
+            "sclk_mhz": num(pick.get("current_gfxclk")),
+            "sclk_per_xcd_mhz": [num(v) for v in xcd] if isinstance(xcd, (list, tuple)) else None,
+            "mclk_mhz": num(pick.get("current_uclk")),
+            "socket_power_w": num(pick.get("current_socket_power")),
+            "gfx_activity_pct": num(pick.get("average_gfx_activity")),
+            "under_load": bool(under_load),
+            "method": (f"amdsmi gpu_metrics (SMU-reported, refreshed ~1/s) read every 20 ms over {seconds:.1f} s of "
+                       "back-to-back launches after the timed region; last refresh >= 1.05 s into the load"),
+        }
+        if errors:
+            out["error"] = errors[0]
+        return out
+    except Exception as exc:
+        return {"error": f"amdsmi query failed: {exc}"}
+    finally:
+        try:
+            amdsmi.amdsmi_shut_down()
+        except Exception:
+            pass
 
 
 def cpu_baseline(cfg, a, b, target_s: float) -> dict:
@@ -322,6 +427,7 @@ def main() -> int:
     roofline["kernel"] = kernel_name
     roofline["traffic"], roofline["traffic_source"] = measured_traffic(kernel_name, cfg.name)
     roofline["per_launch_us"] = per_launch * 1e6
+    roofline["median_single_launch_us"] = median_launch(torch, stream, step, 200) * 1e6
     roofline["algorithmic_per_launch"] = cfg.algorithmic_bytes if is_skinny else cfg.flops
 
     result = {
@@ -350,6 +456,7 @@ def main() -> int:
         },
         "pct_mfma_fp16_peak": 100.0 * tflops / PEAK_F16_TFLOPS,
         "roofline": roofline,
+        "board": board_state(torch, stream, step, 2.5),
     }
     del ta, tb, tc
     if not args.no_extra:

@@ -270,6 +270,55 @@ def test_runs_are_bit_identical(algo, m):
         assert np.array_equal(first.view(np.uint32), _gemm(a, b, algo).view(np.uint32))
 
 
+# Operands whose rows are not 16-byte aligned (odd K or N, odd row strides,
+# 2-byte aligned starts), forced onto 256x192 tiles: the repack's zero
+# padding must cover every tail (K and N down to 1 element past a chunk).
+UNALIGNED_SHAPES = [(601, 713, 1027), (513, 200, 353), (300, 8, 5), (300, 9, 1), (17, 8, 1), (40, 8, 352),
+             (257, 193, 320), (600, 1001, 2049), (300, 7, 40)]
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("m,n,k", UNALIGNED_SHAPES)
+def test_unaligned_operands_integer_bit_exact(m, n, k, dtype):
+    """Small-integer inputs make every summation order exact, so the
+    repacked operands must give A @ B bit for bit, tails included."""
+    rng = np.random.default_rng(m * 7 + n * 3 + k)
+    ai = rng.integers(-4, 5, size=(m, k))
+    bi = rng.integers(-4, 5, size=(k, n))
+    if dtype == "float16":
+        a, b = ai.astype(np.float16), bi.astype(np.float16)
+    else:
+        a, b = oracle.f32_to_bf16_bits(ai.astype(np.float32)), oracle.f32_to_bf16_bits(bi.astype(np.float32))
+    print(f"case unaligned integer {dtype} m={m} n={n} k={k}", flush=True)
+    assert np.array_equal(_gemm(a, b, "tiled_256x192", dtype), (ai @ bi).astype(np.float32))
+
+
+@pytest.mark.parametrize("m,n,k,pad_a,pad_b", [(601, 713, 1027, 3, 1), (333, 270, 150, 9, 5), (300, 8, 40, 1, 7),
+                                               (4095, 3001, 1027, 0, 0)])
+def test_unaligned_strided_views_against_oracle(m, n, k, pad_a, pad_b):
+    """Column-sliced views with odd row strides and 2-byte aligned starts,
+    C into a NaN guard band, against the oracle's float32 fold."""
+    import hc.gfx950 as g
+    from hc.gfx950.workloads import make_inputs
+
+    a, b = make_inputs("c2_4096_f16", seed=m + n + k, m=m, n=n, k=k)
+    big_a = torch.zeros((m, k + pad_a + 1), dtype=torch.float16, device=DEV)
+    big_b = torch.zeros((k, n + pad_b + 1), dtype=torch.float16, device=DEV)
+    va, vb = big_a[:, 1 : k + 1], big_b[:, 1 : n + 1]
+    va.copy_(_dev(a))
+    vb.copy_(_dev(b))
+    guard = torch.full((m + 2, n + 3), float("nan"), dtype=torch.float32, device=DEV)
+    vc = guard[1 : m + 1, 1 : n + 1]
+    print(f"case unaligned views m={m} n={n} k={k}", flush=True)
+    g.gemm(va, vb, out=vc, algo="tiled_256x192")
+    torch.cuda.synchronize()
+    host = guard.cpu().numpy()
+    _check(host[1 : m + 1, 1 : n + 1], oracle.gemm_c(a, b), k)
+    mask = np.ones_like(host, dtype=bool)
+    mask[1 : m + 1, 1 : n + 1] = False
+    assert np.all(np.isnan(host[mask]))
+
+
 @pytest.mark.parametrize("algo", ["auto"] + TILE_ALGOS)
 def test_strided_views_and_guard_band(algo):
     """A and B as column-sliced views (lda > K, ldb > N, 2-byte aligned
