@@ -17,10 +17,11 @@
 //     transposing LDS loads (ds_read_b64_tr_b16), XOR-swizzled
 //     bank-conflict-free layouts, XCD-aware tile order, masked M/N/K tails
 //     by the buffer range check, and an LDS-staged 16-byte epilogue.
-//   * gemm_stream_kernel -- M <= 16 with aligned operands (HBM-bound).  B
+//   * gemm_stream_kernel -- M <= 128 with aligned operands (HBM-bound).  B
 //     streams HBM -> LDS once through a DMA ring, split over K across
-//     workgroups mapped so every XCD covers all column residues; the split
-//     partials are summed in a fixed order (deterministic).
+//     workgroups mapped so every XCD covers all column residues, against
+//     1, 2, 4 or 8 16-row blocks of A; the split partials are summed in a
+//     fixed order (deterministic).
 //   * gemm_generic_kernel -- fallback for operands whose byte offsets do not
 //     fit 31 bits: plain pointers, register staging, any alignment.
 //   * gemm_skinny_kernel -- M <= 16 with unaligned operands: B streamed with
@@ -894,10 +895,12 @@ __global__ __launch_bounds__(kSkinnyThreads) void gemm_skinny_kernel(SkinnyArgs 
 // segments, the strip width that streams best on this part), kStStages deep.
 // Wave w owns columns 32w .. 32w+31: per stage it reads its B operands with
 // transposing LDS loads (ds_read_b64_tr_b16) and issues 2 MFMA 16x16x32
-// against the 16-row A block (rows >= M read as zero).  A's 16x32 slice of
-// each stage arrives by one more DMA instruction (wave 0).
+// against each of the R 16-row blocks of A (R = 1, 2, 4, 8 for M up to 16,
+// 32, 64, 128; rows >= M read as zero), so every B fragment read from LDS
+// feeds R MFMAs.  Each block's 16x32 slice of a stage arrives by one more
+// DMA instruction (block rb from wave rb % 4).
 //
-// Split-K partials go to a workspace [splits][16][N] and stream_reduce_kernel
+// Split-K partials go to a workspace [splits][16 R][N] and stream_reduce_kernel
 // sums them in order s = 0..S-1 (bit-reproducible).  A second launch is
 // cheaper here than an in-kernel last-arrival reduction: that needs either a
 // device-wide L2 write-back/invalidate per workgroup (agent-scope fences) or
@@ -908,26 +911,27 @@ constexpr int kStN = 128;
 constexpr int kStStep = 32;
 constexpr int kStStages = 8;
 constexpr int kStBBytes = kStStep * kStN * 2;  // 8 KB
-constexpr int kStABytes = 16 * kStStep * 2;    // 1 KB
+constexpr int kStABytes = 16 * kStStep * 2;    // 1 KB per 16-row block of A
+constexpr int kStMaxRowBlocks = 8;              // M <= 128
 constexpr int kStMaxSplits = 16;
 
 struct StreamArgs {
   const uint16_t* A;
   const uint16_t* B;
   float* C;
-  float* ws;      // [splits][16][N] partial sums (splits > 1)
+  float* ws;      // [splits][16 * row blocks][N] partial sums (splits > 1)
   int lda, ldb;   // elements, multiples of 8
   int64_t ldc;
   int M, N, K;
   int kchunk;     // rows per split, multiple of kStStep
   int splits;     // 1 .. kStMaxSplits
+  int rblocks;    // 16-row blocks of A: 1, 2, 4 or 8 (M <= 16 * rblocks)
   int a_bytes, b_bytes;
   bool c_vec;     // C rows 16-byte aligned at every 4th column
 };
 
-#define HCG_ST_STAGE(i)                                                             \
-  __shared__ __attribute__((aligned(1024))) unsigned char g_stb##i[kStBBytes];   \
-  __shared__ __attribute__((aligned(1024))) unsigned char g_sta##i[kStABytes];
+#define HCG_ST_STAGE(i) \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_stb##i[kStBBytes];
 HCG_ST_STAGE(0)
 HCG_ST_STAGE(1)
 HCG_ST_STAGE(2)
@@ -937,6 +941,21 @@ HCG_ST_STAGE(5)
 HCG_ST_STAGE(6)
 HCG_ST_STAGE(7)
 #undef HCG_ST_STAGE
+// A stages, one set per row-block count R (a kernel allocates only its own).
+#define HCG_ST_ASTAGES(r)                                                                  \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_sta##r##_0[kStABytes * r];   \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_sta##r##_1[kStABytes * r];   \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_sta##r##_2[kStABytes * r];   \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_sta##r##_3[kStABytes * r];   \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_sta##r##_4[kStABytes * r];   \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_sta##r##_5[kStABytes * r];   \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_sta##r##_6[kStABytes * r];   \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_sta##r##_7[kStABytes * r];
+HCG_ST_ASTAGES(1)
+HCG_ST_ASTAGES(2)
+HCG_ST_ASTAGES(4)
+HCG_ST_ASTAGES(8)
+#undef HCG_ST_ASTAGES
 
 template <int S>
 __device__ __forceinline__ unsigned char* st_b() {
@@ -949,25 +968,38 @@ __device__ __forceinline__ unsigned char* st_b() {
   else if constexpr (S == 6) return g_stb6;
   else return g_stb7;
 }
-template <int S>
+#define HCG_ST_ASEL(r)                          \
+  if constexpr (S == 0) return g_sta##r##_0;     \
+  else if constexpr (S == 1) return g_sta##r##_1; \
+  else if constexpr (S == 2) return g_sta##r##_2; \
+  else if constexpr (S == 3) return g_sta##r##_3; \
+  else if constexpr (S == 4) return g_sta##r##_4; \
+  else if constexpr (S == 5) return g_sta##r##_5; \
+  else if constexpr (S == 6) return g_sta##r##_6; \
+  else return g_sta##r##_7;
+template <int R, int S>
 __device__ __forceinline__ unsigned char* st_a() {
-  if constexpr (S == 0) return g_sta0;
-  else if constexpr (S == 1) return g_sta1;
-  else if constexpr (S == 2) return g_sta2;
-  else if constexpr (S == 3) return g_sta3;
-  else if constexpr (S == 4) return g_sta4;
-  else if constexpr (S == 5) return g_sta5;
-  else if constexpr (S == 6) return g_sta6;
-  else return g_sta7;
+  static_assert(R == 1 || R == 2 || R == 4 || R == 8, "row blocks");
+  if constexpr (R == 1) {
+    HCG_ST_ASEL(1)
+  } else if constexpr (R == 2) {
+    HCG_ST_ASEL(2)
+  } else if constexpr (R == 4) {
+    HCG_ST_ASEL(4)
+  } else {
+    HCG_ST_ASEL(8)
+  }
 }
+#undef HCG_ST_ASEL
 
 // A stage: 16 rows x 32 k (64-byte rows of 4 chunks); chunk c of row r is
 // stored at c ^ ((r >> 2) & 3), so the 16 rows read at one chunk hit 16
 // distinct 16-byte bank groups.
 __device__ __forceinline__ int sta_swz(int row, int c) { return c ^ ((row >> 2) & 3); }
 
-template <int DT>
+template <int DT, int R>
 __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
+  static_assert(R >= 1 && R <= kStMaxRowBlocks, "row blocks");
   constexpr int NB = kStN;
   constexpr int kRowBytes = NB * 2;           // bytes per staged B row
   constexpr int kRowsPerDma = 1024 / kRowBytes;
@@ -1014,10 +1046,19 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
     b_row[i] = (n0 + cb * 8 < g.N) ? kr : 0x3fffffff;
     b_off[i] = (kr * g.ldb + n0 + cb * 8) * 2;
   }
+  // A: 16-row block rb (of R) is loaded by wave rb % 4, lane l covering row
+  // 16 rb + l/4 at physical chunk l%4; a wave loads kAPer or kAPer - 1 blocks.
+  constexpr int kAPer = (R + 3) / 4;
   const int a_r = lane >> 2;
   const int a_c = sta_swz(a_r, lane & 3);
-  const bool a_ok = a_r < g.M;
-  const int a_off = (a_r * g.lda + a_c * 8) * 2;
+  bool a_ok[kAPer];
+  int a_off[kAPer];
+#pragma unroll
+  for (int i = 0; i < kAPer; ++i) {
+    const int row = 16 * (wave + 4 * i) + a_r;
+    a_ok[i] = wave + 4 * i < R && row < g.M;
+    a_off[i] = (row * g.lda + a_c * 8) * 2;
+  }
 
   auto issue = [&](auto sc, int step) {
     constexpr int S = decltype(sc)::value;
@@ -1027,9 +1068,12 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
       const int off = dma_offset(k0 + b_row[i] < kend, b_off[i] + k0 * g.ldb * 2);
       dma16(rsrc_b, (lds_void*)(st_b<S>() + (wave * kDmaPerWave + i) * 1024), off);
     }
-    if (wave == 0) {
-      const int off = dma_offset(a_ok && k0 + a_c * 8 < kend, a_off + k0 * 2);
-      dma16(rsrc_a, (lds_void*)st_a<S>(), off);
+#pragma unroll
+    for (int i = 0; i < kAPer; ++i) {
+      if (wave + 4 * i < R) {
+        const int off = dma_offset(a_ok[i] && k0 + a_c * 8 < kend, a_off[i] + k0 * 2);
+        dma16(rsrc_a, (lds_void*)(st_a<R, S>() + (wave + 4 * i) * kStABytes), off);
+      }
     }
   };
 
@@ -1048,13 +1092,17 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
       fb[j][h] = krow * kRowBytes + b_chunk_swz(krow, ncol >> 3) * 16 + (ncol & 7) * 2;
     }
 
-  f32x4 acc[kBlocks];
+  f32x4 acc[R][kBlocks];
 #pragma unroll
-  for (int j = 0; j < kBlocks; ++j) acc[j] = f32x4{};
+  for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+    for (int j = 0; j < kBlocks; ++j) acc[rb][j] = f32x4{};
 
   auto compute = [&](auto sc) {
     constexpr int S = decltype(sc)::value;
-    const u32x4 af = *reinterpret_cast<const u32x4*>(st_a<S>() + fa);
+    u32x4 af[R];
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb) af[rb] = *reinterpret_cast<const u32x4*>(st_a<R, S>() + rb * kStABytes + fa);
 #pragma unroll
     for (int j = 0; j < kBlocks; ++j) {
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -1063,21 +1111,25 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
           (__attribute__((address_space(3))) s16x4*)(st_b<S>() + fb[j][1]));
       const uint64_t l64 = __builtin_bit_cast(uint64_t, lo), h64 = __builtin_bit_cast(uint64_t, hi);
       const u32x4 bf = u32x4{(uint32_t)l64, (uint32_t)(l64 >> 32), (uint32_t)h64, (uint32_t)(h64 >> 32)};
-      acc[j] = mfma16x16x32<DT>(af, bf, acc[j]);
+#pragma unroll
+      for (int rb = 0; rb < R; ++rb) acc[rb][j] = mfma16x16x32<DT>(af[rb], bf, acc[rb][j]);
     }
   };
 
   // One step from stage S: wait for it (this wave's DMAs; kStStages - 2
   // newer stages may still be in flight), barrier (everyone's DMAs landed and
   // everyone finished the stage being refilled), refill the previous stage
-  // with step + kStStages - 1, multiply.  Wave 0 has one more DMA per stage.
+  // with step + kStStages - 1, multiply.  Waves below R % 4 load one more A
+  // block per stage than the others.
   constexpr int kLater = kStStages - 2;
   auto step_fn = [&](auto sc, int step) {
     constexpr int S = decltype(sc)::value;
-    if (wave == 0) {
-      wait_vmcnt<(kDmaPerWave + 1) * kLater>();
+    if constexpr (R % 4 == 0) {
+      wait_vmcnt<(kDmaPerWave + R / 4) * kLater>();
+    } else if (wave < R % 4) {
+      wait_vmcnt<(kDmaPerWave + R / 4 + 1) * kLater>();
     } else {
-      wait_vmcnt<kDmaPerWave * kLater>();
+      wait_vmcnt<(kDmaPerWave + R / 4) * kLater>();
     }
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
@@ -1120,27 +1172,32 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
   const int ocol = n0 + wave * kColsPerWave + (lane & 15);
   if (g.splits == 1) {
 #pragma unroll
-    for (int j = 0; j < kBlocks; ++j)
+    for (int rb = 0; rb < R; ++rb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = (lane >> 4) * 4 + r, col = ocol + 16 * j;
-        if (row < g.M && col < g.N) g.C[(int64_t)row * g.ldc + col] = acc[j][r];
-      }
+      for (int j = 0; j < kBlocks; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * rb + (lane >> 4) * 4 + r, col = ocol + 16 * j;
+          if (row < g.M && col < g.N) g.C[(int64_t)row * g.ldc + col] = acc[rb][j][r];
+        }
     return;
   }
 #pragma unroll
-  for (int j = 0; j < kBlocks; ++j)
+  for (int rb = 0; rb < R; ++rb)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = (lane >> 4) * 4 + r, col = ocol + 16 * j;
-      if (col < g.N) g.ws[((int64_t)split * 16 + row) * g.N + col] = acc[j][r];
-    }
+    for (int j = 0; j < kBlocks; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * rb + (lane >> 4) * 4 + r, col = ocol + 16 * j;
+        if (col < g.N) g.ws[((int64_t)split * 16 * R + row) * g.N + col] = acc[rb][j][r];
+      }
 }
 
-// C[i][j] = sum over splits s = 0..S-1 (in order) of ws[s][i][j], four
-// columns per thread (N is a multiple of 8 on this path).
+// C[i][j] = sum over splits s = 0..S-1 (in order) of ws[s][i][j] (ws rows:
+// `mrows` per split), four columns per thread (N is a multiple of 8 on this
+// path).
 __global__ __launch_bounds__(256) void stream_reduce_kernel(const float* ws, float* C, int64_t ldc, int M,
-                                                            int N, int splits, bool c_vec) {
+                                                            int N, int mrows, int splits, bool c_vec) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t per_row = N / 4;
   if (idx >= (int64_t)M * per_row) return;
@@ -1148,7 +1205,7 @@ __global__ __launch_bounds__(256) void stream_reduce_kernel(const float* ws, flo
   f32x4 part[kStMaxSplits];
 #pragma unroll
   for (int sp = 0; sp < kStMaxSplits; ++sp)
-    if (sp < splits) part[sp] = *reinterpret_cast<const f32x4*>(ws + ((int64_t)sp * 16 + row) * N + col);
+    if (sp < splits) part[sp] = *reinterpret_cast<const f32x4*>(ws + ((int64_t)sp * mrows + row) * N + col);
   f32x4 v = part[0];
 #pragma unroll
   for (int sp = 1; sp < kStMaxSplits; ++sp)
@@ -1415,26 +1472,39 @@ int launch_stream(const StreamArgs& a, hipStream_t stream) {
   // mapping in gemm_stream_kernel); padding workgroups exit at once.
   const int nblocks = (a.N + kStN - 1) / kStN;
   const dim3 grid((unsigned)(round_up(nblocks, 8) * a.splits));
-  gemm_stream_kernel<DT><<<grid, dim3(256), 0, stream>>>(a);
+  switch (a.rblocks) {
+    case 1: gemm_stream_kernel<DT, 1><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 2: gemm_stream_kernel<DT, 2><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 4: gemm_stream_kernel<DT, 4><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 8: gemm_stream_kernel<DT, 8><<<grid, dim3(256), 0, stream>>>(a); break;
+    default: return set_error(HCG_EINVAL, "internal: %d row blocks", a.rblocks);
+  }
   HCG_HIP_CHECK(hipGetLastError());
   if (a.splits > 1) {
     const int64_t total = (int64_t)a.M * (a.N / 4);
-    stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(a.ws, a.C, a.ldc, a.M, a.N,
-                                                                             a.splits, a.c_vec);
+    stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
+        a.ws, a.C, a.ldc, a.M, a.N, 16 * a.rblocks, a.splits, a.c_vec);
     HCG_HIP_CHECK(hipGetLastError());
   }
   return HCG_OK;
 }
 
+// 16-row blocks of A the streaming kernel runs with for M rows (M <= 128).
+int stream_rblocks(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8; }
+
+// The streaming kernel masks at 8-element granularity through the buffer
+// range check: it needs aligned rows, K and N multiples of 8, and byte
+// offsets below 2^31 for every row block it reads.
+bool stream_fits(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K) {
+  const int64_t kLimit = (int64_t)1 << 31;
+  return M <= 16 * kStMaxRowBlocks && aligned16(A) && lda % 8 == 0 && K % 8 == 0 && aligned16(B) &&
+         ldb % 8 == 0 && N % 8 == 0 && ((int64_t)16 * stream_rblocks(M) * lda + K) * 2 < kLimit &&
+         ((int64_t)round_up(K, kStStep) * ldb + round_up(N, kStN)) * 2 < kLimit;
+}
+
 int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
                float* C, int64_t ldc, int M, int N, int K, hipStream_t stream) {
-  const int64_t kLimit = (int64_t)1 << 31;
-  // The streaming kernel masks at 8-element granularity through the buffer
-  // range check: it needs aligned rows and K, N multiples of 8.
-  const bool stream_ok = aligned16(A) && lda % 8 == 0 && K % 8 == 0 && aligned16(B) && ldb % 8 == 0 &&
-                         N % 8 == 0 && ((int64_t)16 * lda + K) * 2 < kLimit &&
-                         ((int64_t)round_up(K, kStStep) * ldb + round_up(N, kStN)) * 2 < kLimit;
-  if (stream_ok) {
+  if (stream_fits(A, lda, B, ldb, M, N, K)) {
     StreamArgs a{};
     a.A = static_cast<const uint16_t*>(A);
     a.B = static_cast<const uint16_t*>(B);
@@ -1449,19 +1519,26 @@ int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const voi
     const int ksteps = (K + kStStep - 1) / kStStep;
     a.kchunk = ((ksteps + a.splits - 1) / a.splits) * kStStep;
     a.splits = (K + a.kchunk - 1) / a.kchunk;  // drop empty trailing splits
+    a.rblocks = stream_rblocks(M);
     a.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda + K) * 2, 16);
     a.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * ldb + N) * 2, 16);
     a.c_vec = aligned16(C) && ldc % 4 == 0;
     a.ws = nullptr;
     if (a.splits > 1) {
       void* ws = nullptr;
-      const int rc = stream_workspace(st, stream, (size_t)a.splits * 16 * (size_t)N * sizeof(float), &ws);
+      const int rc = stream_workspace(st, stream, (size_t)a.splits * 16 * a.rblocks * (size_t)N * sizeof(float),
+                                      &ws);
       if (rc != HCG_OK) return rc;
       a.ws = static_cast<float*>(ws);
     }
     return dtype == HCG_F16 ? launch_stream<HCG_F16>(a, stream) : launch_stream<HCG_BF16>(a, stream);
   }
-  // Fallback for unaligned operands: register-staged kernel + reduce kernel.
+  // Fallback for unaligned operands (M <= 16): register-staged kernel +
+  // reduce kernel.
+  if (M > 16)
+    return set_error(HCG_EINVAL,
+                     "the skinny kernel needs 16-byte aligned rows and K, N multiples of 8 for M > 16 "
+                     "(M=%d)", M);
   SkinnyArgs a{};
   a.A = static_cast<const uint16_t*>(A);
   a.B = static_cast<const uint16_t*>(B);
@@ -1597,8 +1674,8 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
   if (M > kMaxExtent || N > kMaxExtent || K > kMaxExtent)
     return set_error(HCG_EINVAL, "extent above 2^30: M=%lld N=%lld K=%lld", (long long)M,
                      (long long)N, (long long)K);
-  if (algo == HCG_ALGO_SKINNY && M > 16)
-    return set_error(HCG_EINVAL, "the skinny kernel needs M <= 16, got M=%lld", (long long)M);
+  if (algo == HCG_ALGO_SKINNY && M > 16 * kStMaxRowBlocks)
+    return set_error(HCG_EINVAL, "the skinny kernel needs M <= 128, got M=%lld", (long long)M);
   if (M == 0 || N == 0) {
     t_last_error.clear();
     return HCG_OK;
@@ -1623,7 +1700,11 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
     return HCG_OK;
   }
 
-  const bool use_skinny = algo == HCG_ALGO_SKINNY || (algo == HCG_ALGO_AUTO && M <= 16);
+  // M <= 16, and M <= 128 where the streaming kernel applies, is HBM-bound:
+  // B is streamed once through a skinny kernel instead of occupying only
+  // N/128 workgroups of the tiled kernel.
+  const bool use_skinny = algo == HCG_ALGO_SKINNY ||
+                          (algo == HCG_ALGO_AUTO && (M <= 16 || stream_fits(A, lda, B, ldb, M, N, K)));
   if (use_skinny) {
     rc = run_skinny(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream);
   } else {

@@ -48,7 +48,7 @@ extern "C" {
 /* Kernel selection for hcg_gemm_algo. */
 #define HCG_ALGO_AUTO 0
 #define HCG_ALGO_TILED 1  /* LDS-tiled MFMA kernel, tile shape picked by size (compute-bound shapes) */
-#define HCG_ALGO_SKINNY 2 /* split-K streaming kernel for M <= 16 (HBM-bound shapes) */
+#define HCG_ALGO_SKINNY 2 /* split-K streaming kernel for M <= 128 (HBM-bound shapes) */
 #define HCG_ALGO_GENERIC 3 /* pointer-based tiled kernel: any alignment and size (fallback) */
 /* The LDS-tiled kernel with a fixed output tile shape (rows x columns). */
 #define HCG_ALGO_TILED_256x256 4
@@ -69,7 +69,8 @@ int hcg_gemm(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, 
 
 /* Same as hcg_gemm with an explicit kernel choice (HCG_ALGO_*).  Used by
  * tests and the benchmark to exercise each kernel; HCG_ALGO_SKINNY rejects
- * M > 16 with HCG_EINVAL. */
+ * M > 128, and M > 16 with rows that are not 16-byte aligned or K, N not
+ * multiples of 8, with HCG_EINVAL. */
 int hcg_gemm_algo(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
                   float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
 

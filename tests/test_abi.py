@@ -39,7 +39,7 @@ def test_library_loads_and_exports_every_declared_symbol():
         ((0, 5, None, 0, None, 0, None, 0, 1, 1, 1, None), "dtype must be"),
         ((9, 0, None, 0, None, 0, None, 0, 1, 1, 1, None), "unknown algo"),
         ((0, 0, None, 0, None, 0, None, 0, -1, 1, 1, None), "negative extent"),
-        ((2, 0, None, 0, None, 0, None, 0, 17, 1, 1, None), "needs M <= 16"),
+        ((2, 0, None, 0, None, 0, None, 0, 129, 1, 1, None), "needs M <= 128"),
         ((0, 0, None, 0, None, 0, None, 0, 2, 2, 2, None), "C is NULL"),
         ((0, 0, 0x1000, 2, 0x1000, 2, 0x1000, 1, 2, 2, 2, None), r"ldc \(1\) < N \(2\)"),
         ((0, 0, 0x1000, 1, 0x1000, 2, 0x1000, 2, 2, 2, 2, None), r"lda \(1\) < K \(2\)"),

@@ -230,6 +230,46 @@ def test_skinny_split_and_block_mapping(m, n, k):
     _check(_gemm(a, b, "skinny"), oracle.gemm_c(a, b), k)
 
 
+# M up to 128 streams B once through the skinny kernel with 1, 2, 4 or 8
+# 16-row blocks of A (rows past M load as zero and are never stored).
+@pytest.mark.parametrize("m", [17, 24, 32, 33, 48, 64, 65, 100, 128])
+@pytest.mark.parametrize("n,k", [(8192, 8192), (1000, 336), (256, 1024), (4104, 520)])
+@pytest.mark.parametrize("algo", ["auto", "skinny"])
+def test_skinny_row_blocks(m, n, k, algo):
+    from hc.gfx950.workloads import make_inputs
+
+    print(f"case skinny rows {algo} m={m} n={n} k={k}", flush=True)
+    a, b = make_inputs("c4_skinny_f16", seed=m * 5 + n + k, m=m, n=n, k=k)
+    _check(_gemm(a, b, algo), oracle.gemm_c(a, b), k)
+
+
+@pytest.mark.parametrize("m", [20, 40, 72, 128])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_skinny_row_blocks_integer_bit_exact(m, dtype):
+    rng = np.random.default_rng(m)
+    ai = rng.integers(-4, 5, size=(m, 2048))
+    bi = rng.integers(-4, 5, size=(2048, 1024))
+    if dtype == "float16":
+        a, b = ai.astype(np.float16), bi.astype(np.float16)
+    else:
+        a, b = oracle.f32_to_bf16_bits(ai.astype(np.float32)), oracle.f32_to_bf16_bits(bi.astype(np.float32))
+    print(f"case skinny rows integer {dtype} m={m}", flush=True)
+    assert np.array_equal(_gemm(a, b, "skinny", dtype), (ai @ bi).astype(np.float32))
+
+
+def test_skinny_rows_need_aligned_operands_or_fall_back_to_tiles():
+    """Above 16 rows the skinny path is the streaming kernel only: an
+    explicit request with unaligned rows is a LaunchError, while auto
+    takes the tiled kernel for the same operands."""
+    from hc import LaunchError
+    from hc.gfx950.workloads import make_inputs
+
+    a, b = make_inputs("c4_skinny_f16", seed=3, m=40, n=1001, k=333)
+    with pytest.raises(LaunchError, match="aligned rows"):
+        _gemm(a, b, "skinny")
+    _check(_gemm(a, b, "auto"), oracle.gemm_c(a, b), 333)
+
+
 def test_skinny_repeated_launches_alternating_shapes():
     """The per-stream workspace is reused across launches of different
     shapes: each result matches the oracle, and the same input gives the
