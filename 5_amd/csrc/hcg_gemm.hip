@@ -16,7 +16,9 @@
 //     (buffer_load ... lds), B kept row-major in LDS and read with
 //     transposing LDS loads (ds_read_b64_tr_b16), XOR-swizzled
 //     bank-conflict-free layouts, XCD-aware tile order, masked M/N/K tails
-//     by the buffer range check, and an LDS-staged 16-byte epilogue.
+//     by the buffer range check, and an LDS-staged 16-byte epilogue; shapes
+//     with few tiles and a long K split K over workgroups (partials summed
+//     in a fixed order by stream_reduce_kernel).
 //   * gemm_stream_kernel -- M <= 128 with aligned operands (HBM-bound).  B
 //     streams HBM -> LDS once through a DMA ring, split over K across
 //     workgroups mapped so every XCD covers all column residues, against
@@ -156,9 +158,8 @@ __device__ __forceinline__ int swz(int row, int chunk) {
 // XCDs (id % 8); the first remap gives each XCD a contiguous run of logical
 // tiles, the second orders logical tiles in groups of kGroupM tile rows so
 // that tiles sharing an XCD's L2 also share A rows and B columns.
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn, int wg) {
   const int nt = tiles_m * tiles_n;
-  const int wg = blockIdx.x;
   const int per = nt >> 3, rem = nt & 7, xcd = wg & 7, idx = wg >> 3;
   const int logical =
       (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(kTiledThreads) void gemm_generic_kernel(TiledArgs g
   const int wm = wave >> 1, wn = wave & 1;
 
   int tm, tn;
-  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+  tile_coords(g.tiles_m, g.tiles_n, tm, tn, blockIdx.x);
   const int m0 = tm * kTileM, n0 = tn * kTileN;
   const int nk = (g.K + kTileK - 1) / kTileK;
 
@@ -294,6 +295,11 @@ struct FastArgs {
   int tiles_m, tiles_n;
   int a_bytes, b_bytes;  // buffer extents for the hardware range check
   bool c_vec;            // C rows are 16-byte aligned at every 4th column
+  // Split-K (splits > 1): workgroup s * tiles + t computes tile t over K
+  // rows [s * kchunk, (s + 1) * kchunk) into ws + s * M * N (row stride N).
+  int splits, kchunk;
+  float* ws;
+  bool ws_vec;           // N is a multiple of 4 (16-byte partial rows)
 };
 
 // Scheduling-group masks for __builtin_amdgcn_sched_group_barrier.
@@ -404,8 +410,26 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
+  int wg = blockIdx.x;
+  if (g.splits > 1) {
+    // This split's K range becomes the whole problem: shifted operand bases
+    // and range-check extents (rows past M and columns past N stay past
+    // them), K cut to the range, and C redirected to the split's partial.
+    const int ntiles = g.tiles_m * g.tiles_n;
+    const int split = wg / ntiles;
+    wg -= split * ntiles;
+    const int kbeg = split * g.kchunk;
+    g.A += kbeg;
+    g.B += (int64_t)kbeg * g.ldb;
+    g.a_bytes -= kbeg * 2;
+    g.b_bytes -= kbeg * g.ldb * 2;
+    g.K = min(g.K - kbeg, g.kchunk);
+    g.C = g.ws + (int64_t)split * g.M * g.N;
+    g.ldc = g.N;
+    g.c_vec = g.ws_vec;
+  }
   int tm, tn;
-  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+  tile_coords(g.tiles_m, g.tiles_n, tm, tn, wg);
   const int m0 = tm * TM, n0 = tn * TN;
   const int nk = (g.K + kDmaK - 1) / kDmaK;
 
@@ -1275,9 +1299,11 @@ struct DeviceState {
 DeviceState g_devices[kMaxDevices];
 std::once_flag g_global_once;
 int g_skinny_splits_override = 0;
+int g_tiled_splits_override = 0;  // HCG_TILED_SPLITS: split count for the tiled kernel, if valid
 
 void global_init() {
   if (const char* s = getenv("HCG_SKINNY_SPLITS")) g_skinny_splits_override = atoi(s);
+  if (const char* s = getenv("HCG_TILED_SPLITS")) g_tiled_splits_override = atoi(s);
 }
 
 int current_device_state(DeviceState** out) {
@@ -1376,29 +1402,71 @@ constexpr int kNumTileShapes = sizeof(kTileShapes) / sizeof(kTileShapes[0]);
 // where two workgroups share a CU and each hides part of the other's.  The
 // constants were fitted to 24 shapes timed with every tile shape forced;
 // the pick was within 6% of the fastest on all of them.
-int pick_tile_shape(int num_cus, int M, int N, int K) {
-  const double nk = (double)((K + kDmaK - 1) / kDmaK);
-  int best = 0;
-  double best_cost = 0;
+//
+// With splits > 1 (split-K), each tile's K range is cut into `splits`
+// parts run by separate workgroups whose partial products a second kernel
+// sums in a fixed order; that reduction is charged as its launch plus the
+// partials' HBM traffic ((splits + 1) x M x N floats), converted to K tiles
+// at 0.73 us per 256x256 K tile.
+struct TilePlan {
+  int shape;
+  int splits;
+};
+
+constexpr int kSplitCandidates[] = {1, 2, 3, 4, 6, 8};
+constexpr int kMinKTilesPerSplit = 8;
+constexpr size_t kMaxSplitWorkspace = (size_t)512 << 20;
+
+bool split_ok(int splits, int M, int N, int K) {
+  const int nk = (K + kDmaK - 1) / kDmaK;
+  return splits == 1 || (splits <= 64 && N % 4 == 0 && (nk + splits - 1) / splits >= kMinKTilesPerSplit &&
+                         (size_t)splits * M * N * sizeof(float) <= kMaxSplitWorkspace);
+}
+
+double plan_cost(const TileShape& t, int splits, int num_cus, int M, int N, int K) {
+  const int64_t nk = (K + kDmaK - 1) / kDmaK;
+  const int64_t tiles = (int64_t)((M + t.tm - 1) / t.tm) * ((N + t.tn - 1) / t.tn) * splits;
+  const int64_t per_cu = (tiles + num_cus - 1) / num_cus;
+  const int64_t rounds = (per_cu + t.per_cu - 1) / t.per_cu;
+  const double fixed = t.per_cu == 1 ? 8.0 : 4.0;
+  const double unit = 256.0 * 256.0;
+  double cost = (double)per_cu * t.tm * t.tn * (double)((nk + splits - 1) / splits) / t.eff + (double)rounds * fixed * unit;
+  if (splits > 1) {
+    const double reduce_us = 2.0 + (double)(splits + 1) * M * N * sizeof(float) / 4.5e6;
+    cost += reduce_us / 0.73 * unit;
+  }
+  return cost;
+}
+
+TilePlan plan_tiles(int num_cus, int M, int N, int K, int force_shape, bool allow_split) {
+  TilePlan best{force_shape >= 0 ? force_shape : 0, 1};
+  double best_cost = -1;
+  const int forced_splits =
+      allow_split && g_tiled_splits_override > 0 && split_ok(g_tiled_splits_override, M, N, K)
+          ? g_tiled_splits_override
+          : 0;
   for (int i = 0; i < kNumTileShapes; ++i) {
+    if (force_shape >= 0 && i != force_shape) continue;
     const TileShape& t = kTileShapes[i];
-    const int64_t tiles = (int64_t)((M + t.tm - 1) / t.tm) * ((N + t.tn - 1) / t.tn);
-    if (tiles > 0x7fffffff) continue;
-    const int64_t per_cu = (tiles + num_cus - 1) / num_cus;
-    const int64_t rounds = (per_cu + t.per_cu - 1) / t.per_cu;
-    const double fixed = t.per_cu == 1 ? 8.0 : 4.0;
-    const double cost = (double)per_cu * t.tm * t.tn * nk / t.eff + (double)rounds * fixed * 256 * 256;
-    if (best_cost == 0 || cost < best_cost) {
-      best = i;
-      best_cost = cost;
+    if ((int64_t)((M + t.tm - 1) / t.tm) * ((N + t.tn - 1) / t.tn) * 64 > 0x7fffffff) continue;
+    for (int c = 0; c < (forced_splits > 0 ? 1 : (int)(sizeof(kSplitCandidates) / sizeof(int))); ++c) {
+      const int splits = forced_splits > 0 ? forced_splits : kSplitCandidates[c];
+      if (splits > 1 && !allow_split) break;
+      if (!split_ok(splits, M, N, K)) continue;
+      const double cost = plan_cost(t, splits, num_cus, M, N, K);
+      if (best_cost < 0 || cost < best_cost) {
+        best = TilePlan{i, splits};
+        best_cost = cost;
+      }
     }
   }
   return best;
 }
 
+
 template <int DT>
 int launch_dma(const FastArgs& a, int shape, hipStream_t stream) {
-  const dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
+  const dim3 grid((unsigned)(a.tiles_m * a.tiles_n * (a.splits > 1 ? a.splits : 1)));
   const dim3 block(kTiledThreads);
   switch (shape) {
     case 0: gemm_dma_kernel<DT, 256, 256, 4><<<grid, block, 0, stream>>>(a); break;
@@ -1611,16 +1679,26 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
   const bool fits = fast_extent_a(M, K, lda_p) < kLimit && fast_extent_b(N, K, ldb_p) < kLimit &&
                     tiles <= 0x7fffffff;
   if (force_generic || !fits) return run_generic(dtype, A, lda, B, ldb, C, ldc, M, N, K, stream);
+  // Explicit tile shapes run without a K split; "auto" and "tiled" may split.
+  const TilePlan plan = plan_tiles(st->num_cus, M, N, K, force_shape, force_shape < 0);
+  const TileShape& ts = kTileShapes[plan.shape];
+  if ((int64_t)((M + ts.tm - 1) / ts.tm) * ((N + ts.tn - 1) / ts.tn) * plan.splits > 0x7fffffff)
+    return run_generic(dtype, A, lda, B, ldb, C, ldc, M, N, K, stream);
 
+  // Workspace: repacked operands (rows not 16-byte aligned), then the split
+  // partials [splits][M][N].
+  const size_t a_sz = a_ok ? 0 : round_up((size_t)M * lda_p * 2, 256);
+  const size_t b_sz = b_ok ? 0 : round_up((size_t)K * ldb_p * 2, 256);
+  const size_t p_sz = plan.splits > 1 ? (size_t)plan.splits * M * N * sizeof(float) : 0;
+  void* ws = nullptr;
+  if (a_sz + b_sz + p_sz > 0) {
+    const int rc = stream_workspace(st, stream, a_sz + b_sz + p_sz, &ws);
+    if (rc != HCG_OK) return rc;
+  }
   const uint16_t* a_use = static_cast<const uint16_t*>(A);
   const uint16_t* b_use = static_cast<const uint16_t*>(B);
   if (!a_ok || !b_ok) {
     // Unaligned rows: repack into zero-padded, 16-byte aligned copies.
-    const size_t a_sz = a_ok ? 0 : round_up((size_t)M * lda_p * 2, 256);
-    const size_t b_sz = b_ok ? 0 : round_up((size_t)K * ldb_p * 2, 256);
-    void* ws = nullptr;
-    const int rc = stream_workspace(st, stream, a_sz + b_sz, &ws);
-    if (rc != HCG_OK) return rc;
     uint16_t* a_p = static_cast<uint16_t*>(ws);
     uint16_t* b_p = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + a_sz);
     RepackJob ja{}, jb{};
@@ -1647,10 +1725,6 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
   f.M = M;
   f.N = N;
   f.K = K;
-  const int shape = force_shape >= 0 ? force_shape : pick_tile_shape(st->num_cus, M, N, K);
-  const TileShape& ts = kTileShapes[shape];
-  if ((int64_t)((M + ts.tm - 1) / ts.tm) * ((N + ts.tn - 1) / ts.tn) > 0x7fffffff)
-    return run_generic(dtype, A, lda, B, ldb, C, ldc, M, N, K, stream);
   f.tiles_m = (M + ts.tm - 1) / ts.tm;
   f.tiles_n = (N + ts.tn - 1) / ts.tn;
   // Range-check extents cover the last valid element, rounded up to the
@@ -1658,7 +1732,23 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
   f.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda_p + K) * 2, 16);
   f.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * ldb_p + N) * 2, 16);
   f.c_vec = aligned16(C) && ldc % 4 == 0;
-  return dtype == HCG_F16 ? launch_dma<HCG_F16>(f, shape, stream) : launch_dma<HCG_BF16>(f, shape, stream);
+  f.splits = 1;
+  if (plan.splits > 1) {
+    // K cut into equal runs of whole 32-row K tiles; no split is empty.
+    const int nk = (K + kDmaK - 1) / kDmaK;
+    f.kchunk = (nk + plan.splits - 1) / plan.splits * kDmaK;
+    f.splits = (K + f.kchunk - 1) / f.kchunk;
+    f.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + a_sz + b_sz);
+    f.ws_vec = N % 4 == 0;
+  }
+  const int rc = dtype == HCG_F16 ? launch_dma<HCG_F16>(f, plan.shape, stream)
+                                  : launch_dma<HCG_BF16>(f, plan.shape, stream);
+  if (rc != HCG_OK || f.splits == 1) return rc;
+  const int64_t total = (int64_t)M * (N / 4);
+  stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(f.ws, C, ldc, M, N, M, f.splits,
+                                                                           aligned16(C) && ldc % 4 == 0);
+  HCG_HIP_CHECK(hipGetLastError());
+  return HCG_OK;
 }
 
 int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,

@@ -5,8 +5,8 @@ The reference runs concurrent launches from two threads
 through the C ABI.  Graph capture: the kernels take no host-side action
 inside a launch except on a stream's first use of a workspace size (an
 allocation), so after one warm-up call on the capture stream every path --
-tiled, skinny split-K (workspace partials + reduce) and repacked ragged
-operands (workspace copies) -- records into a graph.  Every replay is
+tiled, skinny split-K (workspace partials + reduce), tiled split-K and
+repacked ragged operands (workspace copies) -- records into a graph.  Every replay is
 checked against the eager result, with eager work between replays.
 """
 
@@ -36,6 +36,7 @@ CASES = [
     ("tiled", 1024, 768, 512),
     ("skinny", 16, 4096, 4096),
     ("ragged", 1000, 601, 333),
+    ("splitk", 512, 512, 16384),
 ]
 
 

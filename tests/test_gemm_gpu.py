@@ -270,6 +270,38 @@ def test_skinny_rows_need_aligned_operands_or_fall_back_to_tiles():
     _check(_gemm(a, b, "auto"), oracle.gemm_c(a, b), 333)
 
 
+# Few output tiles and a long K: the tiled kernel splits K over several
+# workgroups per tile and sums their partials in a fixed order.  Shapes
+# include ragged M/N tails, a last split shorter than the others, unaligned
+# rows (repacked operands feeding the split) and bf16.
+SPLITK_SHAPES = [(1024, 1024, 8192), (512, 512, 16384), (700, 900, 12000), (200, 8000, 8200), (1500, 1500, 4104),
+                 (333, 444, 9999), (1024, 4096, 16384)]
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("m,n,k", SPLITK_SHAPES)
+def test_split_k_against_oracle(m, n, k, dtype):
+    from hc.gfx950.workloads import make_inputs
+
+    print(f"case split-k {dtype} m={m} n={n} k={k}", flush=True)
+    cfg = "c2_4096_f16" if dtype == "float16" else "c3_8192_bf16"
+    a, b = make_inputs(cfg, seed=m + 2 * n + k, m=m, n=n, k=k)
+    want = oracle.gemm_c(a, b, oracle.F16 if dtype == "float16" else oracle.BF16)
+    _check(_gemm(a, b, "auto", dtype), want, k)
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 512, 16384), (300, 1000, 8200)])
+def test_split_k_integer_bit_exact_and_reproducible(m, n, k):
+    rng = np.random.default_rng(k)
+    ai = rng.integers(-3, 4, size=(m, k))
+    bi = rng.integers(-3, 4, size=(k, n))
+    a, b = ai.astype(np.float16), bi.astype(np.float16)
+    print(f"case split-k integer m={m} n={n} k={k}", flush=True)
+    first = _gemm(a, b)
+    assert np.array_equal(first, (ai @ bi).astype(np.float32))
+    assert np.array_equal(first.view(np.uint32), _gemm(a, b).view(np.uint32))
+
+
 def test_skinny_repeated_launches_alternating_shapes():
     """The per-stream workspace is reused across launches of different
     shapes: each result matches the oracle, and the same input gives the
