@@ -47,10 +47,10 @@ extern "C" {
 
 /* Kernel selection for hcg_gemm_algo. */
 #define HCG_ALGO_AUTO 0
-#define HCG_ALGO_TILED 1  /* LDS-tiled MFMA kernel, tile shape picked by size (compute-bound shapes) */
+#define HCG_ALGO_TILED 1  /* LDS-tiled MFMA kernel, tile shape and K split picked by shape (compute-bound) */
 #define HCG_ALGO_SKINNY 2 /* split-K streaming kernel for M <= 128 (HBM-bound shapes) */
 #define HCG_ALGO_GENERIC 3 /* pointer-based tiled kernel: any alignment and size (fallback) */
-/* The LDS-tiled kernel with a fixed output tile shape (rows x columns). */
+/* The LDS-tiled kernel with a fixed output tile shape (rows x columns), never split along K. */
 #define HCG_ALGO_TILED_256x256 4
 #define HCG_ALGO_TILED_256x192 5
 #define HCG_ALGO_TILED_128x256 6
