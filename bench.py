@@ -65,9 +65,10 @@ def parse_args() -> argparse.Namespace:
 
 
 def measured_traffic(kernel: str, workload: str) -> tuple[int | None, str | None]:
-    """HBM-side bytes per launch from the committed rocprofv3 summary
+    """Memory-side bytes per launch from the committed rocprofv3 summary
     profiles/<kernel>_<workload>.md (FETCH_SIZE and WRITE_SIZE runs, each
-    scaled by a plain-copy calibration), or (None, None) if absent."""
+    scaled by a plain-copy calibration; the L2's traffic to the fabric, of
+    which the Infinity Cache may serve part), or (None, None) if absent."""
     path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}.md")
     if not os.path.exists(path):
         return None, None
