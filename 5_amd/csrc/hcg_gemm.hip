@@ -45,6 +45,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <vector>
 #include <type_traits>
 #include <string>
 
@@ -1279,11 +1280,16 @@ constexpr int kMaxDevices = 64;
 constexpr int kMaxStreamWorkspaces = 16;
 
 // Library-owned scratch (split-K partials, repacked operands), one grow-only
-// buffer per (device, stream) so that concurrent streams never share it.
+// buffer per (device, stream) so that concurrent streams never share it.  A
+// buffer handed out while its stream is being captured into a HIP graph is
+// pinned: the graph keeps its address, so it is never freed or reused for
+// another stream afterwards; when its slot needs a larger or a different
+// buffer, the pinned one is retired (kept allocated until the process ends).
 struct Workspace {
   void* stream = nullptr;
   void* ptr = nullptr;
   size_t bytes = 0;
+  bool pinned = false;
 };
 
 struct DeviceState {
@@ -1294,6 +1300,7 @@ struct DeviceState {
   std::mutex ws_mutex;
   Workspace ws[kMaxStreamWorkspaces];
   int ws_next = 0;
+  std::vector<void*> retired;  // pinned buffers replaced in their slot
 };
 
 DeviceState g_devices[kMaxDevices];
@@ -1328,6 +1335,11 @@ int current_device_state(DeviceState** out) {
 }
 
 int stream_workspace(DeviceState* st, hipStream_t stream, size_t bytes, void** out) {
+  // The null stream is never captured (and querying it during another
+  // stream's capture is itself an error), so only real streams are asked.
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (stream != nullptr) HCG_HIP_CHECK(hipStreamIsCapturing(stream, &capture));
+  const bool capturing = capture == hipStreamCaptureStatusActive;
   std::lock_guard<std::mutex> lock(st->ws_mutex);
   Workspace* w = nullptr;
   for (auto& cand : st->ws)
@@ -1344,9 +1356,14 @@ int stream_workspace(DeviceState* st, hipStream_t stream, size_t bytes, void** o
     st->ws_next = (st->ws_next + 1) % kMaxStreamWorkspaces;
   }
   if (w->ptr && (w->stream != (void*)stream || w->bytes < bytes)) {
-    HCG_HIP_CHECK(hipFree(w->ptr));
+    if (w->pinned) {
+      st->retired.push_back(w->ptr);
+    } else {
+      HCG_HIP_CHECK(hipFree(w->ptr));
+    }
     w->ptr = nullptr;
     w->bytes = 0;
+    w->pinned = false;
   }
   if (!w->ptr) {
     void* p = nullptr;
@@ -1356,6 +1373,7 @@ int stream_workspace(DeviceState* st, hipStream_t stream, size_t bytes, void** o
     w->bytes = want;
   }
   w->stream = (void*)stream;
+  if (capturing) w->pinned = true;
   *out = w->ptr;
   return HCG_OK;
 }

@@ -105,3 +105,38 @@ def test_graph_capture_replays_match_eager(name, m, n, k):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i}"
+
+
+def test_graph_replays_stay_valid_after_the_stream_needs_a_larger_workspace():
+    """A captured graph keeps the workspace address it was captured with:
+    when a later eager call on the same stream needs a larger workspace,
+    the library allocates a new one and keeps the captured one alive, so
+    replays still compute the right result."""
+    import hc.gfx950 as g
+
+    s = torch.cuda.Stream(device=DEV)
+    a, b = _inputs("skinny", 16, 4096, 4096, seed=31)
+    ta, tb = _dev(a), _dev(b)
+    out = torch.empty((16, 4096), dtype=torch.float32, device=DEV)
+    with torch.cuda.stream(s):
+        g.gemm(ta, tb, out=out)
+    s.synchronize()
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        g.gemm(ta, tb, out=out)
+    # a split-K call whose partials (8 x 512 x 512 floats) exceed the
+    # captured workspace, on the capturing stream
+    big_a, big_b = _inputs("tiled", 512, 512, 16384, seed=32)
+    tba, tbb = _dev(big_a), _dev(big_b)
+    with torch.cuda.stream(s):
+        big = g.gemm(tba, tbb)
+    s.synchronize()
+    rep = oracle.parity_check(big.cpu().numpy(), oracle.gemm_c(big_a, big_b), 16384)
+    assert rep.ok, str(rep)
+    print("case graph replay after workspace growth", flush=True)
+    for i in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
