@@ -24,8 +24,9 @@
 //     workgroups mapped so every XCD covers all column residues, against
 //     1, 2, 4 or 8 16-row blocks of A; the split partials are summed in a
 //     fixed order (deterministic).
-//   * gemm_generic_kernel -- fallback for operands whose byte offsets do not
-//     fit 31 bits: plain pointers, register staging, any alignment.
+//   * gemm_generic_kernel -- fallback (plain pointers, register staging, any
+//     alignment) for unaligned operands whose byte offsets do not fit 31
+//     bits; aligned ones that large run the DMA kernel's WIDE form.
 //   * gemm_skinny_kernel -- M <= 16 with unaligned operands: B streamed with
 //     128-bit loads, transposed 8x8 in registers, split over K; partial sums
 //     reduced in a fixed order.
@@ -394,7 +395,12 @@ __device__ __forceinline__ int b_chunk_swz(int k, int c) {
   return c ^ ((m >> 1) * 10 + (m & 1) * 4);
 }
 
-template <int DT, int TM, int TN, int STAGES>
+// WIDE: operands whose byte offsets reach 2^31.  The A resource then starts
+// at the tile's first row and the B resource at (k0, n0), rebuilt for every
+// B issue, with extents that end at the last valid element of that range,
+// so every offset stays small; the range check still zero-fills rows past
+// M and K, and chunks past N are redirected past the extent.
+template <int DT, int TM, int TN, int STAGES, bool WIDE = false>
 __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_kernel(FastArgs g) {
   static_assert((TM == 256 && STAGES == 4) || (TM == 128 && STAGES == 3), "tile variant");
   static_assert(TN == 256 || TN == 192 || TN == 128, "tile width");
@@ -434,8 +440,11 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
   const int m0 = tm * TM, n0 = tn * TN;
   const int nk = (g.K + kDmaK - 1) / kDmaK;
 
-  const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(g.A, g.a_bytes);
+  const __amdgpu_buffer_rsrc_t rsrc_a =
+      WIDE ? make_rsrc(g.A + (int64_t)m0 * g.lda, ((min(g.M - m0, TM) - 1) * g.lda + g.K) * 2)
+           : make_rsrc(g.A, g.a_bytes);
   const __amdgpu_buffer_rsrc_t rsrc_b = make_rsrc(g.B, g.b_bytes);
+  const int a_row0 = WIDE ? 0 : m0;  // A rows are counted from the resource base
 
   // DMA roles.  Each wave instruction fills 1 KB of LDS, lane l at byte
   // 16*l.  A: wave w owns 16-row blocks kADma*w .. +kADma-1; lane l covers
@@ -451,7 +460,7 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
     const int row = blk * 16 + (lane >> 2);
     const int c = a_chunk_swz(row, lane & 3);
     a_col[i] = c * 8;
-    a_off[i] = ((m0 + row) * g.lda + c * 8) * 2;
+    a_off[i] = ((a_row0 + row) * g.lda + c * 8) * 2;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -463,7 +472,10 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
     // offset at the end of B so the unchecked issue below reads zeros too.
     const bool live = cb < TN / 8 && n0 + cb * 8 < g.N;
     b_row[i] = live ? kr : 0x3fffffff;
-    b_off[i] = live ? (kr * g.ldb + n0 + cb * 8) * 2 : g.b_bytes;
+    if constexpr (WIDE)
+      b_off[i] = live ? (kr * g.ldb + cb * 8) * 2 : kOobOffset;
+    else
+      b_off[i] = live ? (kr * g.ldb + n0 + cb * 8) * 2 : g.b_bytes;
   }
 
   // The A part (kADma loads) or B part (4 loads) of tile kt into stage sc.
@@ -490,13 +502,23 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
   auto issue_b = [&](auto sc, auto full, int kt) {
     unsigned char* st = dma_stage<TM, decltype(sc)::value>();
     const int k0 = kt * kDmaK;
+    if constexpr (WIDE) {
+      // Resource for rows k0 .. k0 + 31 from column n0; rows past K are past
+      // its extent (empty once k0 >= K).
+      const int rows = min(kDmaK, g.K - k0);
+      const __amdgpu_buffer_rsrc_t rk =
+          make_rsrc(g.B + (int64_t)k0 * g.ldb + n0, rows > 0 ? ((rows - 1) * g.ldb + (g.N - n0)) * 2 : 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      lds_void* dst = (lds_void*)(st + kABytes + (wave * 4 + i) * 1024);
-      if constexpr (decltype(full)::value)
-        dma16(rsrc_b, dst, b_off[i], k0 * g.ldb * 2);
-      else
-        dma16(rsrc_b, dst, dma_offset(k0 + b_row[i] < g.K, b_off[i] + k0 * g.ldb * 2));
+      for (int i = 0; i < 4; ++i) dma16(rk, (lds_void*)(st + kABytes + (wave * 4 + i) * 1024), b_off[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        lds_void* dst = (lds_void*)(st + kABytes + (wave * 4 + i) * 1024);
+        if constexpr (decltype(full)::value)
+          dma16(rsrc_b, dst, b_off[i], k0 * g.ldb * 2);
+        else
+          dma16(rsrc_b, dst, dma_offset(k0 + b_row[i] < g.K, b_off[i] + k0 * g.ldb * 2));
+      }
     }
   };
 
@@ -1482,15 +1504,15 @@ TilePlan plan_tiles(int num_cus, int M, int N, int K, int force_shape, bool allo
 }
 
 
-template <int DT>
+template <int DT, bool WIDE>
 int launch_dma(const FastArgs& a, int shape, hipStream_t stream) {
   const dim3 grid((unsigned)(a.tiles_m * a.tiles_n * (a.splits > 1 ? a.splits : 1)));
   const dim3 block(kTiledThreads);
   switch (shape) {
-    case 0: gemm_dma_kernel<DT, 256, 256, 4><<<grid, block, 0, stream>>>(a); break;
-    case 1: gemm_dma_kernel<DT, 256, 192, 4><<<grid, block, 0, stream>>>(a); break;
-    case 2: gemm_dma_kernel<DT, 128, 256, 3><<<grid, block, 0, stream>>>(a); break;
-    default: gemm_dma_kernel<DT, 128, 128, 3><<<grid, block, 0, stream>>>(a); break;
+    case 0: gemm_dma_kernel<DT, 256, 256, 4, WIDE><<<grid, block, 0, stream>>>(a); break;
+    case 1: gemm_dma_kernel<DT, 256, 192, 4, WIDE><<<grid, block, 0, stream>>>(a); break;
+    case 2: gemm_dma_kernel<DT, 128, 256, 3, WIDE><<<grid, block, 0, stream>>>(a); break;
+    default: gemm_dma_kernel<DT, 128, 128, 3, WIDE><<<grid, block, 0, stream>>>(a); break;
   }
   HCG_HIP_CHECK(hipGetLastError());
   return HCG_OK;
@@ -1696,7 +1718,32 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
   const int64_t tiles = (int64_t)((M + kTileM - 1) / kTileM) * ((N + kTileN - 1) / kTileN);
   const bool fits = fast_extent_a(M, K, lda_p) < kLimit && fast_extent_b(N, K, ldb_p) < kLimit &&
                     tiles <= 0x7fffffff;
-  if (force_generic || !fits) return run_generic(dtype, A, lda, B, ldb, C, ldc, M, N, K, stream);
+  // Aligned operands too large for 32-bit offsets from their base run the
+  // WIDE form (per-tile / per-K-tile resources) when one 256-row panel of A
+  // and one 32-row panel of B stay below 2^31 bytes.
+  const bool wide = !fits && a_ok && b_ok && (int64_t)kTileM * lda * 2 < kLimit &&
+                    (int64_t)kDmaK * ldb * 2 < kLimit && tiles <= 0x7fffffff;
+  if (force_generic || (!fits && !wide)) return run_generic(dtype, A, lda, B, ldb, C, ldc, M, N, K, stream);
+  if (wide) {
+    const TilePlan plan = plan_tiles(st->num_cus, M, N, K, force_shape, false);
+    const TileShape& ts = kTileShapes[plan.shape];
+    FastArgs f{};
+    f.A = static_cast<const uint16_t*>(A);
+    f.B = static_cast<const uint16_t*>(B);
+    f.C = C;
+    f.lda = (int)lda;
+    f.ldb = (int)ldb;
+    f.ldc = ldc;
+    f.M = M;
+    f.N = N;
+    f.K = K;
+    f.tiles_m = (M + ts.tm - 1) / ts.tm;
+    f.tiles_n = (N + ts.tn - 1) / ts.tn;
+    f.c_vec = aligned16(C) && ldc % 4 == 0;
+    f.splits = 1;
+    return dtype == HCG_F16 ? launch_dma<HCG_F16, true>(f, plan.shape, stream)
+                            : launch_dma<HCG_BF16, true>(f, plan.shape, stream);
+  }
   // Explicit tile shapes run without a K split; "auto" and "tiled" may split.
   const TilePlan plan = plan_tiles(st->num_cus, M, N, K, force_shape, force_shape < 0);
   const TileShape& ts = kTileShapes[plan.shape];
@@ -1759,8 +1806,8 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
     f.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + a_sz + b_sz);
     f.ws_vec = N % 4 == 0;
   }
-  const int rc = dtype == HCG_F16 ? launch_dma<HCG_F16>(f, plan.shape, stream)
-                                  : launch_dma<HCG_BF16>(f, plan.shape, stream);
+  const int rc = dtype == HCG_F16 ? launch_dma<HCG_F16, false>(f, plan.shape, stream)
+                                  : launch_dma<HCG_BF16, false>(f, plan.shape, stream);
   if (rc != HCG_OK || f.splits == 1) return rc;
   const int64_t total = (int64_t)M * (N / 4);
   stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(f.ws, C, ldc, M, N, M, f.splits,

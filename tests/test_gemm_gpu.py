@@ -513,3 +513,50 @@ def test_random_shapes_and_layouts_against_oracle(i):
     mask = np.ones_like(host, dtype=bool)
     mask[:m, 1 : n + 1] = False
     assert np.all(np.isnan(host[mask]))
+
+
+# Operands whose byte offsets reach 2^31 (over 2 GiB): the tiled kernel's
+# WIDE form rebases its buffer resources per tile (A) and per 32-row K
+# step (B).  Inputs are periodic small integers built on the device, so the
+# exact product has a closed form that is cheap on the host.
+def test_wide_b_operand_over_2gib_bit_exact():
+    import hc.gfx950 as g
+
+    m, n, k = 200, 16392, 65536  # B: 2.0 GiB + 1 MiB
+    print(f"case wide B m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(5)
+    ai = rng.integers(-3, 4, size=(m, k))
+    kk = torch.arange(k, device=DEV, dtype=torch.int32).view(k, 1)
+    nn = torch.arange(n, device=DEV, dtype=torch.int32).view(1, n)
+    b = ((kk + nn) % 5 - 2).to(torch.float16)  # B[k, j] = ((k + j) mod 5) - 2
+    a = torch.from_numpy(ai.astype(np.float16)).to(DEV)
+    c = g.gemm(a, b)
+    torch.cuda.synchronize()
+    del b
+    # C[i, j] = sum_r (r - 2) * S[i, (r - j) mod 5], S[i, q] = sum of A[i, k] over k = q mod 5
+    s = np.stack([ai[:, q::5].sum(axis=1) for q in range(5)], axis=1)
+    j = np.arange(n)
+    want = sum((r - 2) * s[:, (r - j) % 5] for r in range(5)).astype(np.float32)
+    assert np.array_equal(c.cpu().numpy(), want)
+
+
+def test_wide_a_operand_over_2gib_bit_exact():
+    import hc.gfx950 as g
+
+    m, n, k = 65600, 264, 16384  # A: 2.0 GiB + 3 MiB
+    print(f"case wide A m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(6)
+    bi = rng.integers(-3, 4, size=(k, n))
+    ii = torch.arange(m, device=DEV, dtype=torch.int32).view(m, 1)
+    kk = torch.arange(k, device=DEV, dtype=torch.int32).view(1, k)
+    a = ((ii + 2 * kk) % 7 - 3).to(torch.float16)  # A[i, k] = ((i + 2k) mod 7) - 3
+    b = torch.from_numpy(bi.astype(np.float16)).to(DEV)
+    c = g.gemm(a, b)
+    torch.cuda.synchronize()
+    del a
+    # (i + 2k) mod 7 = r  <=>  k = 4 (r - i) mod 7, so C[i] depends on i mod 7 only
+    t = np.stack([bi[q::7].sum(axis=0) for q in range(7)], axis=0)
+    rows = np.stack([sum((r - 3) * t[(4 * (r - i)) % 7] for r in range(7)) for i in range(7)]).astype(np.float32)
+    got = c.cpu().numpy()
+    for i in range(7):
+        assert np.array_equal(got[i::7], np.broadcast_to(rows[i], got[i::7].shape)), f"rows = {i} mod 7"
