@@ -184,6 +184,12 @@ def gemm(a: Any, b: Any, out: Any | None = None, *, algo: str = "auto", device: 
     their device, asynchronously.  numpy arrays are copied to the device,
     computed, and copied back into ``out`` (created if None); the call then
     returns after the result is on the host.
+
+    ``algo``: "auto" (the library picks: the streaming kernel for M <= 16,
+    and up to 128 rows with 16-byte aligned rows; otherwise the LDS-tiled
+    kernel with a modelled tile shape and K split), "tiled", "skinny",
+    "generic", or a fixed tile shape "tiled_256x256", "tiled_256x192",
+    "tiled_128x256", "tiled_128x128" (never split along K).
     """
     algo_code = _native.ALGOS.get(algo)
     if algo_code is None:
