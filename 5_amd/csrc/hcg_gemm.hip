@@ -403,7 +403,7 @@ __device__ __forceinline__ int b_chunk_swz(int k, int c) {
 template <int DT, int TM, int TN, int STAGES, bool WIDE = false>
 __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_kernel(FastArgs g) {
   static_assert((TM == 256 && STAGES == 4) || (TM == 128 && STAGES == 3), "tile variant");
-  static_assert(TN == 256 || TN == 192 || TN == 128, "tile width");
+  static_assert(TN == 256 || TN == 192 || TN == 128 || TN == 64, "tile width");
   constexpr int kMi = TM / 64;            // 32-row MFMA tiles per wave
   constexpr int kNi = TN / 64;            // 32-column MFMA tiles per wave
   constexpr int kADma = TM / 64;          // A DMA instructions per wave per stage
@@ -1266,14 +1266,15 @@ __global__ __launch_bounds__(256) void stream_reduce_kernel(const float* ws, flo
   }
 }
 
-// C[i][j] = sum over splits s = 0..S-1 (in order) of ws[s][i][j].
+// C[i][j] = sum over splits s = 0..S-1 (in order) of ws[s][i][j] (ws rows:
+// `mrows` per split), one element per thread: any N.
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* ws, float* C, int64_t ldc,
-                                                            int M, int N, int splits) {
+                                                            int M, int N, int mrows, int splits) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)M * N) return;
   const int row = (int)(idx / N), col = (int)(idx % N);
   float v = ws[(int64_t)row * N + col];
-  for (int s = 1; s < splits; ++s) v += ws[((int64_t)s * 16 + row) * N + col];
+  for (int s = 1; s < splits; ++s) v += ws[((int64_t)s * mrows + row) * N + col];
   C[(int64_t)row * ldc + col] = v;
 }
 
@@ -1432,6 +1433,7 @@ constexpr TileShape kTileShapes[] = {
     {256, 192, 1, 0.97f},
     {128, 256, 2, 0.93f},
     {128, 128, 2, 0.75f},
+    {256, 64, 1, 0.75f},  // narrow N (<= 64): the A stream dominates
 };
 constexpr int kNumTileShapes = sizeof(kTileShapes) / sizeof(kTileShapes[0]);
 
@@ -1459,7 +1461,7 @@ constexpr size_t kMaxSplitWorkspace = (size_t)512 << 20;
 
 bool split_ok(int splits, int M, int N, int K) {
   const int nk = (K + kDmaK - 1) / kDmaK;
-  return splits == 1 || (splits <= 64 && N % 4 == 0 && (nk + splits - 1) / splits >= kMinKTilesPerSplit &&
+  return splits == 1 || (splits <= 64 && (nk + splits - 1) / splits >= kMinKTilesPerSplit &&
                          (size_t)splits * M * N * sizeof(float) <= kMaxSplitWorkspace);
 }
 
@@ -1512,7 +1514,8 @@ int launch_dma(const FastArgs& a, int shape, hipStream_t stream) {
     case 0: gemm_dma_kernel<DT, 256, 256, 4, WIDE><<<grid, block, 0, stream>>>(a); break;
     case 1: gemm_dma_kernel<DT, 256, 192, 4, WIDE><<<grid, block, 0, stream>>>(a); break;
     case 2: gemm_dma_kernel<DT, 128, 256, 3, WIDE><<<grid, block, 0, stream>>>(a); break;
-    default: gemm_dma_kernel<DT, 128, 128, 3, WIDE><<<grid, block, 0, stream>>>(a); break;
+    case 3: gemm_dma_kernel<DT, 128, 128, 3, WIDE><<<grid, block, 0, stream>>>(a); break;
+    default: gemm_dma_kernel<DT, 256, 64, 4, WIDE><<<grid, block, 0, stream>>>(a); break;
   }
   HCG_HIP_CHECK(hipGetLastError());
   return HCG_OK;
@@ -1535,7 +1538,7 @@ int launch_skinny(const SkinnyArgs& a, bool vec_a, bool vec_b, hipStream_t strea
   if (a.splits > 1) {
     const int64_t total = (int64_t)a.M * a.N;
     skinny_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(a.ws, a.C, a.ldc, a.M,
-                                                                             a.N, a.splits);
+                                                                             a.N, 16, a.splits);
     HCG_HIP_CHECK(hipGetLastError());
   }
   return HCG_OK;
@@ -1804,14 +1807,19 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
     f.kchunk = (nk + plan.splits - 1) / plan.splits * kDmaK;
     f.splits = (K + f.kchunk - 1) / f.kchunk;
     f.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + a_sz + b_sz);
-    f.ws_vec = N % 4 == 0;
+    f.ws_vec = N % 4 == 0;  // 16-byte partial rows (the workspace base is 256-byte aligned)
   }
   const int rc = dtype == HCG_F16 ? launch_dma<HCG_F16, false>(f, plan.shape, stream)
                                   : launch_dma<HCG_BF16, false>(f, plan.shape, stream);
   if (rc != HCG_OK || f.splits == 1) return rc;
-  const int64_t total = (int64_t)M * (N / 4);
-  stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(f.ws, C, ldc, M, N, M, f.splits,
-                                                                           aligned16(C) && ldc % 4 == 0);
+  if (N % 4 == 0) {
+    const int64_t total = (int64_t)M * (N / 4);
+    stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(f.ws, C, ldc, M, N, M, f.splits,
+                                                                             aligned16(C) && ldc % 4 == 0);
+  } else {
+    const int64_t total = (int64_t)M * N;
+    skinny_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(f.ws, C, ldc, M, N, M, f.splits);
+  }
   HCG_HIP_CHECK(hipGetLastError());
   return HCG_OK;
 }
@@ -1820,7 +1828,7 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
               float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream_ptr) {
   if (dtype != HCG_F16 && dtype != HCG_BF16)
     return set_error(HCG_EINVAL, "dtype must be HCG_F16 (0) or HCG_BF16 (1), got %d", dtype);
-  if (algo < HCG_ALGO_AUTO || algo > HCG_ALGO_TILED_128x128)
+  if (algo < HCG_ALGO_AUTO || algo > HCG_ALGO_TILED_256x64)
     return set_error(HCG_EINVAL, "unknown algo %d", algo);
   if (M < 0 || N < 0 || K < 0)
     return set_error(HCG_EINVAL, "negative extent: M=%lld N=%lld K=%lld", (long long)M,

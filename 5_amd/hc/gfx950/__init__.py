@@ -189,7 +189,7 @@ def gemm(a: Any, b: Any, out: Any | None = None, *, algo: str = "auto", device: 
     and up to 128 rows with 16-byte aligned rows; otherwise the LDS-tiled
     kernel with a modelled tile shape and K split), "tiled", "skinny",
     "generic", or a fixed tile shape "tiled_256x256", "tiled_256x192",
-    "tiled_128x256", "tiled_128x128" (never split along K).
+    "tiled_128x256", "tiled_128x128", "tiled_256x64" (never split along K).
     """
     algo_code = _native.ALGOS.get(algo)
     if algo_code is None:

@@ -35,6 +35,7 @@ HCG_ALGO_TILED_256x256 = 4
 HCG_ALGO_TILED_256x192 = 5
 HCG_ALGO_TILED_128x256 = 6
 HCG_ALGO_TILED_128x128 = 7
+HCG_ALGO_TILED_256x64 = 8
 
 ALGOS = {
     "auto": HCG_ALGO_AUTO,
@@ -45,6 +46,7 @@ ALGOS = {
     "tiled_256x192": HCG_ALGO_TILED_256x192,
     "tiled_128x256": HCG_ALGO_TILED_128x256,
     "tiled_128x128": HCG_ALGO_TILED_128x128,
+    "tiled_256x64": HCG_ALGO_TILED_256x64,
 }
 
 # Every symbol include/hcg_gemm.h and include/hcg_tile_ops.h declare.

@@ -55,6 +55,7 @@ extern "C" {
 #define HCG_ALGO_TILED_256x192 5
 #define HCG_ALGO_TILED_128x256 6
 #define HCG_ALGO_TILED_128x128 7
+#define HCG_ALGO_TILED_256x64 8
 
 /* Idempotent one-time set-up (device properties).  Replaces the reference's
  * once-per-process registration, lib/CAPI/HC.cpp:22-29.  Optional: every

@@ -167,7 +167,7 @@ def test_large_tile_variant_integer_bit_exact():
     assert np.array_equal(got, (ai @ bi).astype(np.float32))
 
 
-TILE_ALGOS = ["tiled_256x256", "tiled_256x192", "tiled_128x256", "tiled_128x128"]
+TILE_ALGOS = ["tiled_256x256", "tiled_256x192", "tiled_128x256", "tiled_128x128", "tiled_256x64"]
 
 
 @pytest.mark.parametrize("algo", TILE_ALGOS)
@@ -300,6 +300,19 @@ def test_split_k_integer_bit_exact_and_reproducible(m, n, k):
     first = _gemm(a, b)
     assert np.array_equal(first, (ai @ bi).astype(np.float32))
     assert np.array_equal(first.view(np.uint32), _gemm(a, b).view(np.uint32))
+
+
+# Narrow N (few output columns, e.g. low-rank projections): 256x64 tiles
+# over M with a K split, including N not a multiple of 4 (partials summed
+# one element at a time) and unaligned K.
+@pytest.mark.parametrize("m,n,k", [(4096, 13, 8192), (16384, 8, 16384), (5000, 7, 5000), (3000, 1, 9000),
+                                   (4096, 64, 4096), (8000, 33, 2048), (2048, 3, 777)])
+def test_narrow_n_against_oracle(m, n, k):
+    from hc.gfx950.workloads import make_inputs
+
+    print(f"case narrow n m={m} n={n} k={k}", flush=True)
+    a, b = make_inputs("c2_4096_f16", seed=m + n + k, m=m, n=n, k=k)
+    _check(_gemm(a, b), oracle.gemm_c(a, b), k)
 
 
 def test_skinny_repeated_launches_alternating_shapes():
