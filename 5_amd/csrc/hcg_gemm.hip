@@ -1240,8 +1240,231 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
       }
 }
 
+// ---------------------------------------------------------------------------
+// Narrow-N streaming kernel: A through LDS by DMA in 256-byte row pieces
+// ---------------------------------------------------------------------------
+//
+// For N <= 32 the product is bound by reading A (M x K) once, and the
+// tiled kernel's 64-byte row pieces per 32-wide K step stream poorly.  Here
+// a workgroup (256 threads) takes 64 rows of A over a run of K (split-K
+// when the row blocks alone do not fill the chip); wave w owns rows
+// 16w .. 16w+15 and all NB (16 or 32, >= N) columns.  A moves HBM -> LDS in
+// stages of 128 k -- 256 bytes of each of the 64 rows, 16 KB -- kRsStages
+// deep, and B's 128 x NB slice of each stage comes along (every workgroup
+// reads all of B, which stays in L2).  Per stage a wave issues 4 x NB/16
+// MFMA 16x16x32: A fragments by ds_read_b128 (row l%16, 8 k at chunk l/16,
+// chunks XOR-swizzled by row), B fragments by two transposing reads as in
+// the skinny streaming kernel.  Rows past M, k past the run and columns
+// past N load as zero (range check or redirect); K must be a multiple of 8
+// (a chunk straddling K would pair k >= K of A with zeroed B rows), N need
+// not be (the straddling chunk's extra columns only reach C columns >= N).
+
+constexpr int kRsRows = 64;
+constexpr int kRsStep = 128;
+constexpr int kRsStages = 6;
+constexpr int kRsABytes = kRsRows * kRsStep * 2;  // 16 KB
+constexpr int kRsBBytes = kRsStep * 32 * 2;       // 8 KB (NB <= 32)
+
+struct RowStreamArgs {
+  const uint16_t* A;
+  const uint16_t* B;
+  float* C;
+  float* ws;      // [splits][M][N] partial sums (splits > 1)
+  int lda, ldb;   // elements, multiples of 8
+  int64_t ldc;
+  int M, N, K;
+  int kchunk;     // K per split, multiple of kRsStep
+  int splits;
+  int a_bytes, b_bytes;
+};
+
+#define HCG_RS_STAGE(i)                                                         \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_rsa##i[kRsABytes]; \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_rsb##i[kRsBBytes];
+HCG_RS_STAGE(0)
+HCG_RS_STAGE(1)
+HCG_RS_STAGE(2)
+HCG_RS_STAGE(3)
+HCG_RS_STAGE(4)
+HCG_RS_STAGE(5)
+#undef HCG_RS_STAGE
+
+template <int S>
+__device__ __forceinline__ unsigned char* rs_a() {
+  if constexpr (S == 0) return g_rsa0;
+  else if constexpr (S == 1) return g_rsa1;
+  else if constexpr (S == 2) return g_rsa2;
+  else if constexpr (S == 3) return g_rsa3;
+  else if constexpr (S == 4) return g_rsa4;
+  else return g_rsa5;
+}
+template <int S>
+__device__ __forceinline__ unsigned char* rs_b() {
+  if constexpr (S == 0) return g_rsb0;
+  else if constexpr (S == 1) return g_rsb1;
+  else if constexpr (S == 2) return g_rsb2;
+  else if constexpr (S == 3) return g_rsb3;
+  else if constexpr (S == 4) return g_rsb4;
+  else return g_rsb5;
+}
+
+template <int DT, int NB>
+__global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
+  static_assert(NB == 16 || NB == 32, "column block");
+  constexpr int kChunksB = NB / 8;               // 16-byte chunks per staged B row
+  constexpr int kRowsPerBDma = 64 / kChunksB;    // B rows per DMA instruction
+  constexpr int kBDmaPerWave = kRsStep / kRowsPerBDma / 4;
+  constexpr int kDmaPerWave = 4 + kBDmaPerWave;  // 4 A instructions (16 rows x 256 B)
+  constexpr int kBlocks = NB / 16;               // MFMA column blocks
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nrb = (g.M + kRsRows - 1) / kRsRows;
+  const int split = blockIdx.x / nrb;
+  const int m0 = (blockIdx.x - split * nrb) * kRsRows;
+  const int kbeg = split * g.kchunk;
+  const int kend = min(g.K, kbeg + g.kchunk);
+  const int nsteps = (kend - kbeg + kRsStep - 1) / kRsStep;
+
+  const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(g.A, g.a_bytes);
+  const __amdgpu_buffer_rsrc_t rsrc_b = make_rsrc(g.B, g.b_bytes);
+
+  // DMA roles.  A: wave w loads rows 16w .. 16w+15 in 4 instructions of 4
+  // rows; lane l covers row 4i + l/16 of them at physical chunk l%16, i.e.
+  // logical chunk (l%16) ^ (row%16).  B: wave w loads kBDmaPerWave blocks of
+  // kRowsPerBDma k rows; lane l covers row l / kChunksB, chunk l % kChunksB.
+  int a_off[4], a_col[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * wave + 4 * i + (lane >> 4);
+    const int c = (lane & 15) ^ (row & 15);
+    a_col[i] = c * 8;
+    a_off[i] = ((m0 + row) * g.lda + c * 8) * 2;
+  }
+  int b_off[kBDmaPerWave], b_row[kBDmaPerWave];
+#pragma unroll
+  for (int i = 0; i < kBDmaPerWave; ++i) {
+    const int kr = (wave * kBDmaPerWave + i) * kRowsPerBDma + lane / kChunksB;
+    const int cb = lane % kChunksB;
+    b_row[i] = cb * 8 < g.N ? kr : 0x3fffffff;
+    b_off[i] = (kr * g.ldb + cb * 8) * 2;
+  }
+
+  // Row block rb walks its run of K starting at step rb % nsteps (wrapping):
+  // with all blocks starting at the same k, a power-of-two row stride puts
+  // every concurrent 256-byte piece at the same address offset modulo the
+  // stride, and the reads pile onto a few HBM channels (16384 x 8 x 16384
+  // fp16: 146 us unrotated vs 103 us at K = 16392).  Steps past the run load
+  // zeros.
+  const int rot = (blockIdx.x - split * nrb) % nsteps;
+  auto issue = [&](auto sc, int step) {
+    constexpr int S = decltype(sc)::value;
+    int s = step + rot;
+    if (s >= nsteps) s -= nsteps;
+    const int k0 = step < nsteps ? kbeg + s * kRsStep : kend;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma16(rsrc_a, (lds_void*)(rs_a<S>() + (16 * wave + 4 * i) * 256),
+            dma_offset(k0 + a_col[i] < kend, a_off[i] + k0 * 2));
+#pragma unroll
+    for (int i = 0; i < kBDmaPerWave; ++i)
+      dma16(rsrc_b, (lds_void*)(rs_b<S>() + (wave * kBDmaPerWave + i) * 1024),
+            dma_offset(k0 + b_row[i] < kend, b_off[i] + k0 * g.ldb * 2));
+  };
+
+  // Fragment addresses.  A, k step j: row 16w + l%16, chunk 4j + l/16.  B,
+  // k step j, column block cb, half h: source lane s = l%16 of group
+  // q = l/16 points at k row 32j + 8q + 4h + s/4, column 16cb + 4(s%4).
+  const int a_r = 16 * wave + (lane & 15);
+  int fa[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) fa[j] = a_r * 256 + ((4 * j + (lane >> 4)) ^ (a_r & 15)) * 16;
+  int fb[4][kBlocks][2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int cb = 0; cb < kBlocks; ++cb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int sl = lane & 15, q = lane >> 4;
+        fb[j][cb][h] = (32 * j + 8 * q + 4 * h + (sl >> 2)) * (NB * 2) + (16 * cb + 4 * (sl & 3)) * 2;
+      }
+
+  f32x4 acc[kBlocks];
+#pragma unroll
+  for (int cb = 0; cb < kBlocks; ++cb) acc[cb] = f32x4{};
+
+  auto compute = [&](auto sc) {
+    constexpr int S = decltype(sc)::value;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 af = *reinterpret_cast<const u32x4*>(rs_a<S>() + fa[j]);
+#pragma unroll
+      for (int cb = 0; cb < kBlocks; ++cb) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(rs_b<S>() + fb[j][cb][0]));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(rs_b<S>() + fb[j][cb][1]));
+        const uint64_t l64 = __builtin_bit_cast(uint64_t, lo), h64 = __builtin_bit_cast(uint64_t, hi);
+        const u32x4 bf = u32x4{(uint32_t)l64, (uint32_t)(l64 >> 32), (uint32_t)h64, (uint32_t)(h64 >> 32)};
+        acc[cb] = mfma16x16x32<DT>(af, bf, acc[cb]);
+      }
+    }
+  };
+
+  // Same step structure as the skinny streaming kernel: wait for stage S
+  // (kRsStages - 2 newer stages may be in flight), barrier, refill the
+  // stage freed one step earlier, multiply.
+  constexpr int kLater = kRsStages - 2;
+  auto step_fn = [&](auto sc, int step) {
+    constexpr int S = decltype(sc)::value;
+    wait_vmcnt<kDmaPerWave * kLater>();
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(StageC<(S + kRsStages - 1) % kRsStages>{}, step + kRsStages - 1);
+    compute(sc);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  issue(StageC<0>{}, 0);
+  issue(StageC<1>{}, 1);
+  issue(StageC<2>{}, 2);
+  issue(StageC<3>{}, 3);
+  issue(StageC<4>{}, 4);
+
+  int step = 0;
+  for (; step + kRsStages <= nsteps; step += kRsStages) {
+    step_fn(StageC<0>{}, step);
+    step_fn(StageC<1>{}, step + 1);
+    step_fn(StageC<2>{}, step + 2);
+    step_fn(StageC<3>{}, step + 3);
+    step_fn(StageC<4>{}, step + 4);
+    step_fn(StageC<5>{}, step + 5);
+  }
+  if (step < nsteps) step_fn(StageC<0>{}, step++);
+  if (step < nsteps) step_fn(StageC<1>{}, step++);
+  if (step < nsteps) step_fn(StageC<2>{}, step++);
+  if (step < nsteps) step_fn(StageC<3>{}, step++);
+  if (step < nsteps) step_fn(StageC<4>{}, step++);
+  wait_vmcnt<0>();  // no DMA may still be writing LDS at exit
+
+  // 16x16 accumulator layout: register r of lane l holds row 4*(l/16) + r,
+  // column l%16 of the block.
+  float* dst = g.splits > 1 ? g.ws + (int64_t)split * g.M * g.N : g.C;
+  const int64_t ld = g.splits > 1 ? (int64_t)g.N : g.ldc;
+#pragma unroll
+  for (int cb = 0; cb < kBlocks; ++cb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + 16 * wave + (lane >> 4) * 4 + r, col = 16 * cb + (lane & 15);
+      if (row < g.M && col < g.N) dst[(int64_t)row * ld + col] = acc[cb][r];
+    }
+}
+
 // C[i][j] = sum over splits s = 0..S-1 (in order) of ws[s][i][j] (ws rows:
-// `mrows` per split), four columns per thread (N is a multiple of 8 on this
+// `mrows` per split), four columns per thread (N is a multiple of 4 on this
 // path).
 __global__ __launch_bounds__(256) void stream_reduce_kernel(const float* ws, float* C, int64_t ldc, int M,
                                                             int N, int mrows, int splits, bool c_vec) {
@@ -1678,6 +1901,89 @@ int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const voi
                           : launch_skinny<HCG_BF16>(a, vec_a, vec_b, stream);
 }
 
+// The narrow-N streaming kernel: N <= 32, aligned rows, K a multiple of 8,
+// byte offsets below 2^31.
+// B's rows need not be aligned: B (at most 32 columns) is repacked when they
+// are not.
+bool rowstream_fits(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K) {
+  const int64_t kLimit = (int64_t)1 << 31;
+  const int64_t ldb_use = aligned16(B) && ldb % 8 == 0 ? ldb : round_up(N, 8);
+  return N <= 32 && aligned16(A) && lda % 8 == 0 && K % 8 == 0 &&
+         ((int64_t)round_up(M, kRsRows) * lda + round_up(K, kRsStep)) * 2 < kLimit &&
+         ((int64_t)round_up(K, kRsStep) * ldb_use + 32) * 2 < kLimit;
+}
+
+int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
+                  float* C, int64_t ldc, int M, int N, int K, hipStream_t stream) {
+  RowStreamArgs a{};
+  a.A = static_cast<const uint16_t*>(A);
+  a.B = static_cast<const uint16_t*>(B);
+  a.C = C;
+  a.lda = (int)lda;
+  a.ldb = (int)ldb;
+  a.ldc = ldc;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  // Row blocks, then K splits until the workgroups cover the CUs (each
+  // split at least 4 stages of 128 k).
+  const int nrb = (M + kRsRows - 1) / kRsRows;
+  const int ksteps = (K + kRsStep - 1) / kRsStep;
+  int splits = (st->num_cus + nrb - 1) / nrb;
+  const int max_by_k = ksteps / 4 > 0 ? ksteps / 4 : 1;
+  if (splits > max_by_k) splits = max_by_k;
+  if (splits > 16) splits = 16;
+  if (splits < 1) splits = 1;
+  a.kchunk = (ksteps + splits - 1) / splits * kRsStep;
+  a.splits = (K + a.kchunk - 1) / a.kchunk;
+  // Workspace: B repacked to zero-padded 16-byte aligned rows (when its rows
+  // are not), then the split partials [splits][M][N].
+  const bool b_ok = aligned16(B) && ldb % 8 == 0;
+  const int64_t ldb_use = b_ok ? ldb : round_up(N, 8);
+  const size_t b_sz = b_ok ? 0 : round_up((size_t)K * ldb_use * 2, 256);
+  const size_t p_sz = a.splits > 1 ? (size_t)a.splits * M * N * sizeof(float) : 0;
+  if (b_sz + p_sz > 0) {
+    void* ws = nullptr;
+    const int rc = stream_workspace(st, stream, b_sz + p_sz, &ws);
+    if (rc != HCG_OK) return rc;
+    if (!b_ok) {
+      uint16_t* b_p = static_cast<uint16_t*>(ws);
+      const RepackJob ja{};
+      const RepackJob jb{a.B, ldb, K, N, b_p, (int)ldb_use, (int64_t)K * (ldb_use / 8)};
+      const int64_t per_block = (int64_t)256 * kRepackPer;
+      repack_kernel<<<(unsigned)((jb.chunks + per_block - 1) / per_block), 256, 0, stream>>>(ja, jb);
+      HCG_HIP_CHECK(hipGetLastError());
+      a.B = b_p;
+      a.ldb = (int)ldb_use;
+    }
+    if (a.splits > 1) a.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + b_sz);
+  }
+  a.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda + K) * 2, 16);
+  a.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * a.ldb + N) * 2, 16);
+  const dim3 grid((unsigned)(nrb * a.splits));
+  const bool wide = N > 16;
+  if (dtype == HCG_F16) {
+    if (wide) gemm_rowstream_kernel<HCG_F16, 32><<<grid, dim3(256), 0, stream>>>(a);
+    else gemm_rowstream_kernel<HCG_F16, 16><<<grid, dim3(256), 0, stream>>>(a);
+  } else {
+    if (wide) gemm_rowstream_kernel<HCG_BF16, 32><<<grid, dim3(256), 0, stream>>>(a);
+    else gemm_rowstream_kernel<HCG_BF16, 16><<<grid, dim3(256), 0, stream>>>(a);
+  }
+  HCG_HIP_CHECK(hipGetLastError());
+  if (a.splits > 1) {
+    if (N % 4 == 0) {
+      const int64_t total = (int64_t)M * (N / 4);
+      stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
+          a.ws, C, ldc, M, N, M, a.splits, aligned16(C) && ldc % 4 == 0);
+    } else {
+      const int64_t total = (int64_t)M * N;
+      skinny_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(a.ws, C, ldc, M, N, M, a.splits);
+    }
+    HCG_HIP_CHECK(hipGetLastError());
+  }
+  return HCG_OK;
+}
+
 int run_generic(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, float* C,
                 int64_t ldc, int M, int N, int K, hipStream_t stream) {
   TiledArgs a{};
@@ -1828,7 +2134,7 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
               float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream_ptr) {
   if (dtype != HCG_F16 && dtype != HCG_BF16)
     return set_error(HCG_EINVAL, "dtype must be HCG_F16 (0) or HCG_BF16 (1), got %d", dtype);
-  if (algo < HCG_ALGO_AUTO || algo > HCG_ALGO_TILED_256x64)
+  if (algo < HCG_ALGO_AUTO || algo > HCG_ALGO_NARROW)
     return set_error(HCG_EINVAL, "unknown algo %d", algo);
   if (M < 0 || N < 0 || K < 0)
     return set_error(HCG_EINVAL, "negative extent: M=%lld N=%lld K=%lld", (long long)M,
@@ -1868,7 +2174,17 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
   // N/128 workgroups of the tiled kernel.
   const bool use_skinny = algo == HCG_ALGO_SKINNY ||
                           (algo == HCG_ALGO_AUTO && (M <= 16 || stream_fits(A, lda, B, ldb, M, N, K)));
-  if (use_skinny) {
+  // N <= 32 (and more than 16 rows) is HBM-bound on A: stream A in 256-byte
+  // row pieces.
+  const bool use_narrow = !use_skinny && (algo == HCG_ALGO_NARROW ||
+                                          (algo == HCG_ALGO_AUTO && rowstream_fits(A, lda, B, ldb, M, N, K)));
+  if (algo == HCG_ALGO_NARROW && !rowstream_fits(A, lda, B, ldb, M, N, K))
+    return set_error(HCG_EINVAL,
+                     "the narrow kernel needs N <= 32, 16-byte aligned rows of A and K a multiple of 8 "
+                     "(M=%lld N=%lld K=%lld)", (long long)M, (long long)N, (long long)K);
+  if (use_narrow) {
+    rc = run_rowstream(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream);
+  } else if (use_skinny) {
     rc = run_skinny(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream);
   } else {
     const int force_shape = algo >= HCG_ALGO_TILED_256x256 ? algo - HCG_ALGO_TILED_256x256 : -1;

@@ -52,8 +52,9 @@ class Gfx950Target:
 
     device: GPU index for host (numpy) buffers; device tensors run where they
         live.  None = the current device.
-    algo: "auto" (by shape), "tiled" or "skinny" (M <= 128; above 16 rows
-        only with 16-byte aligned rows and K, N multiples of 8).
+    algo: "auto" (by shape), "tiled", "skinny" (M <= 128; above 16 rows
+        only with 16-byte aligned rows and K, N multiples of 8) or "narrow"
+        (N <= 32, A's rows 16-byte aligned, K a multiple of 8).
     max_group_size: HIP's workgroup limit, checked like the simulator's.
     """
 
@@ -186,10 +187,12 @@ def gemm(a: Any, b: Any, out: Any | None = None, *, algo: str = "auto", device: 
     returns after the result is on the host.
 
     ``algo``: "auto" (the library picks: the streaming kernel for M <= 16,
-    and up to 128 rows with 16-byte aligned rows; otherwise the LDS-tiled
-    kernel with a modelled tile shape and K split), "tiled", "skinny",
-    "generic", or a fixed tile shape "tiled_256x256", "tiled_256x192",
-    "tiled_128x256", "tiled_128x128", "tiled_256x64" (never split along K).
+    and up to 128 rows with 16-byte aligned rows; the narrow streaming
+    kernel for N <= 32 with A's rows aligned and K a multiple of 8;
+    otherwise the LDS-tiled kernel with a modelled tile shape and K split),
+    "tiled", "skinny", "narrow", "generic", or a fixed tile shape
+    "tiled_256x256", "tiled_256x192", "tiled_128x256", "tiled_128x128",
+    "tiled_256x64" (never split along K).
     """
     algo_code = _native.ALGOS.get(algo)
     if algo_code is None:

@@ -36,6 +36,7 @@ HCG_ALGO_TILED_256x192 = 5
 HCG_ALGO_TILED_128x256 = 6
 HCG_ALGO_TILED_128x128 = 7
 HCG_ALGO_TILED_256x64 = 8
+HCG_ALGO_NARROW = 9
 
 ALGOS = {
     "auto": HCG_ALGO_AUTO,
@@ -47,6 +48,7 @@ ALGOS = {
     "tiled_128x256": HCG_ALGO_TILED_128x256,
     "tiled_128x128": HCG_ALGO_TILED_128x128,
     "tiled_256x64": HCG_ALGO_TILED_256x64,
+    "narrow": HCG_ALGO_NARROW,
 }
 
 # Every symbol include/hcg_gemm.h and include/hcg_tile_ops.h declare.

@@ -56,6 +56,10 @@ extern "C" {
 #define HCG_ALGO_TILED_128x256 6
 #define HCG_ALGO_TILED_128x128 7
 #define HCG_ALGO_TILED_256x64 8
+/* Streaming kernel for N <= 32 (A streamed once in 256-byte row pieces, K split to fill the
+ * chip; HBM-bound shapes).  Needs A's rows 16-byte aligned and K a multiple of 8; B may be
+ * any layout (it is repacked when its rows are not aligned). */
+#define HCG_ALGO_NARROW 9
 
 /* Idempotent one-time set-up (device properties).  Replaces the reference's
  * once-per-process registration, lib/CAPI/HC.cpp:22-29.  Optional: every
@@ -71,7 +75,8 @@ int hcg_gemm(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, 
 /* Same as hcg_gemm with an explicit kernel choice (HCG_ALGO_*).  Used by
  * tests and the benchmark to exercise each kernel; HCG_ALGO_SKINNY rejects
  * M > 128, and M > 16 with rows that are not 16-byte aligned or K, N not
- * multiples of 8, with HCG_EINVAL. */
+ * multiples of 8, and HCG_ALGO_NARROW rejects N > 32, A's rows not 16-byte
+ * aligned and K not a multiple of 8, with HCG_EINVAL. */
 int hcg_gemm_algo(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
                   float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
 

@@ -37,7 +37,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     "args,match",
     [
         ((0, 5, None, 0, None, 0, None, 0, 1, 1, 1, None), "dtype must be"),
-        ((9, 0, None, 0, None, 0, None, 0, 1, 1, 1, None), "unknown algo"),
+        ((10, 0, None, 0, None, 0, None, 0, 1, 1, 1, None), "unknown algo"),
         ((0, 0, None, 0, None, 0, None, 0, -1, 1, 1, None), "negative extent"),
         ((2, 0, None, 0, None, 0, None, 0, 129, 1, 1, None), "needs M <= 128"),
         ((0, 0, None, 0, None, 0, None, 0, 2, 2, 2, None), "C is NULL"),

@@ -315,6 +315,69 @@ def test_narrow_n_against_oracle(m, n, k):
     _check(_gemm(a, b), oracle.gemm_c(a, b), k)
 
 
+# N <= 32 with aligned rows: the narrow streaming kernel (A in 256-byte row
+# pieces, row blocks of 64, K split to fill the chip).
+@pytest.mark.parametrize("m,n,k", [(17, 1, 8), (64, 16, 128), (100, 13, 1000), (1000, 32, 4096), (4096, 8, 8192),
+                                   (16384, 16, 16384), (333, 17, 520), (2048, 24, 12000), (65, 3, 136)])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_narrow_streaming_kernel_against_oracle(m, n, k, dtype):
+    from hc.gfx950.workloads import make_inputs
+
+    print(f"case narrow streaming {dtype} m={m} n={n} k={k}", flush=True)
+    cfg = "c2_4096_f16" if dtype == "float16" else "c3_8192_bf16"
+    a, b = make_inputs(cfg, seed=m * 3 + n + k, m=m, n=n, k=k)
+    want = oracle.gemm_c(a, b, oracle.F16 if dtype == "float16" else oracle.BF16)
+    _check(_gemm(a, b, "narrow", dtype), want, k)
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 13, 8192), (300, 32, 2048), (129, 1, 4096)])
+def test_narrow_streaming_integer_bit_exact_and_reproducible(m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    ai = rng.integers(-4, 5, size=(m, k))
+    bi = rng.integers(-4, 5, size=(k, n))
+    a, b = ai.astype(np.float16), bi.astype(np.float16)
+    print(f"case narrow integer m={m} n={n} k={k}", flush=True)
+    first = _gemm(a, b, "narrow")
+    assert np.array_equal(first, (ai @ bi).astype(np.float32))
+    assert np.array_equal(first.view(np.uint32), _gemm(a, b, "narrow").view(np.uint32))
+
+
+def test_narrow_streaming_views_and_guard_band():
+    """Row strides above K and N (multiples of 8), C into a NaN guard band."""
+    import hc.gfx950 as g
+    from hc.gfx950.workloads import make_inputs
+
+    m, n, k = 777, 19, 2056
+    a, b = make_inputs("c2_4096_f16", seed=77, m=m, n=n, k=k)
+    big_a = torch.zeros((m, k + 8), dtype=torch.float16, device=DEV)
+    big_b = torch.zeros((k, 24 + 16), dtype=torch.float16, device=DEV)
+    va, vb = big_a[:, :k], big_b[:, :n]
+    va.copy_(_dev(a))
+    vb.copy_(_dev(b))
+    guard = torch.full((m + 2, n + 3), float("nan"), dtype=torch.float32, device=DEV)
+    vc = guard[1 : m + 1, 1 : n + 1]
+    print("case narrow views", flush=True)
+    g.gemm(va, vb, out=vc, algo="narrow")
+    torch.cuda.synchronize()
+    host = guard.cpu().numpy()
+    _check(host[1 : m + 1, 1 : n + 1], oracle.gemm_c(a, b), k)
+    mask = np.ones_like(host, dtype=bool)
+    mask[1 : m + 1, 1 : n + 1] = False
+    assert np.all(np.isnan(host[mask]))
+
+
+def test_narrow_kernel_rejects_what_it_cannot_run():
+    from hc import LaunchError
+    from hc.gfx950.workloads import make_inputs
+
+    a, b = make_inputs("c2_4096_f16", seed=1, m=100, n=40, k=256)
+    with pytest.raises(LaunchError, match="narrow kernel needs N <= 32"):
+        _gemm(a, b, "narrow")
+    a, b = make_inputs("c2_4096_f16", seed=1, m=100, n=8, k=257)
+    with pytest.raises(LaunchError, match="K a multiple of 8"):
+        _gemm(a, b, "narrow")
+
+
 def test_skinny_repeated_launches_alternating_shapes():
     """The per-stream workspace is reused across launches of different
     shapes: each result matches the oracle, and the same input gives the
