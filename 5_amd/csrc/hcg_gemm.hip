@@ -1580,13 +1580,16 @@ int current_device_state(DeviceState** out) {
   return HCG_OK;
 }
 
+// The caller holds st->ws_mutex from this call until every kernel that uses
+// *out is enqueued: another thread's call (on the same stream, needing more
+// bytes, or evicting the slot) frees the buffer, and hipFree waits only for
+// work already enqueued.
 int stream_workspace(DeviceState* st, hipStream_t stream, size_t bytes, void** out) {
   // The null stream is never captured (and querying it during another
   // stream's capture is itself an error), so only real streams are asked.
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   if (stream != nullptr) HCG_HIP_CHECK(hipStreamIsCapturing(stream, &capture));
   const bool capturing = capture == hipStreamCaptureStatusActive;
-  std::lock_guard<std::mutex> lock(st->ws_mutex);
   Workspace* w = nullptr;
   for (auto& cand : st->ws)
     if (cand.ptr && cand.stream == (void*)stream) w = &cand;
@@ -2182,6 +2185,9 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
     return set_error(HCG_EINVAL,
                      "the narrow kernel needs N <= 32, 16-byte aligned rows of A and K a multiple of 8 "
                      "(M=%lld N=%lld K=%lld)", (long long)M, (long long)N, (long long)K);
+  // Workspaces stay valid while ws_mutex is held (see stream_workspace), so
+  // the lock covers the launches too; a launch only enqueues work.
+  std::lock_guard<std::mutex> lock(st->ws_mutex);
   if (use_narrow) {
     rc = run_rowstream(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream);
   } else if (use_skinny) {

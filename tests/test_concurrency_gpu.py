@@ -5,8 +5,9 @@ The reference runs concurrent launches from two threads
 through the C ABI.  Graph capture: the kernels take no host-side action
 inside a launch except on a stream's first use of a workspace size (an
 allocation), so after one warm-up call on the capture stream every path --
-tiled, skinny split-K (workspace partials + reduce), tiled split-K and
-repacked ragged operands (workspace copies) -- records into a graph.  Every replay is
+tiled, skinny split-K (workspace partials + reduce), tiled split-K,
+repacked ragged operands (workspace copies) and the narrow kernel (repacked
+B, split partials) -- records into a graph.  Every replay is
 checked against the eager result, with eager work between replays.
 """
 
@@ -37,6 +38,7 @@ CASES = [
     ("skinny", 16, 4096, 4096),
     ("ragged", 1000, 601, 333),
     ("splitk", 512, 512, 16384),
+    ("narrow", 2048, 13, 4096),
 ]
 
 
@@ -73,6 +75,45 @@ def test_two_host_threads_each_with_a_stream():
         t.start()
     for t in threads:
         t.join(timeout=60)
+    assert not errors, errors
+    for a, b, _, _, tc in jobs:
+        rep = oracle.parity_check(tc.cpu().numpy(), oracle.gemm_c(a, b), a.shape[1])
+        assert rep.ok, str(rep)
+
+
+def test_two_host_threads_sharing_one_stream():
+    """Both threads enqueue onto one stream, alternating shapes whose
+    library workspaces differ in size, so a call can find the stream's buffer
+    too small and replace it while the other thread's call is between taking
+    that buffer and launching on it (the library's workspace lock covers both)."""
+    import hc.gfx950 as g
+
+    shapes = [("skinny", 16, 2048, 2048), ("splitk", 512, 512, 16384), ("narrow", 2048, 13, 4096),
+              ("ragged", 1000, 601, 333), ("splitk", 768, 768, 12288)]
+    jobs = []
+    for i, (name, m, n, k) in enumerate(shapes * 2):
+        a, b = _inputs(name, m, n, k, seed=300 + i)
+        jobs.append((a, b, _dev(a), _dev(b), torch.empty((m, n), dtype=torch.float32, device=DEV)))
+    shared = torch.cuda.Stream(device=DEV)
+    errors = []
+    barrier = threading.Barrier(2)
+
+    def worker(part):
+        try:
+            barrier.wait()
+            with torch.cuda.stream(shared):
+                for _ in range(10):
+                    for _, _, ta, tb, tc in part:
+                        g.gemm(ta, tb, out=tc)
+        except Exception as exc:  # surfaced below
+            errors.append(exc)
+
+    threads = [threading.Thread(target=worker, args=(jobs[i::2],)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    shared.synchronize()
     assert not errors, errors
     for a, b, _, _, tc in jobs:
         rep = oracle.parity_check(tc.cpu().numpy(), oracle.gemm_c(a, b), a.shape[1])
