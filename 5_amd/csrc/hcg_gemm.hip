@@ -329,10 +329,12 @@ constexpr int kSgDsRead = 0x100;
 // point at 4 consecutive k rows x 16 columns, so lane i receives 4
 // consecutive k of column i, the MFMA B operand.
 //
-// Requirements (checked on the host): A, B 16-byte aligned; lda, ldb, K, N
-// multiples of 8 (or operands repacked to that form with zero padding).
-// Chunks past K or N are redirected past the buffer extent, so the hardware
-// range check returns zeros; rows past M (A) or K (B) are past it already.
+// Requirements (checked on the host): A, B 16-byte aligned; lda, ldb, K
+// multiples of 8 (or operands repacked to that form with zero padding).  N
+// need not be: the chunk holding column N - 1 also loads up to 7 padding
+// columns of B, which reach only C columns >= N (never stored).  Chunks past
+// K or N are redirected past the buffer extent, so the hardware range check
+// returns zeros; rows past M (A) or K (B) are past it already.
 
 constexpr int kDmaK = 32;
 
@@ -397,9 +399,10 @@ __device__ __forceinline__ int b_chunk_swz(int k, int c) {
 
 // WIDE: operands whose byte offsets reach 2^31.  The A resource then starts
 // at the tile's first row and the B resource at (k0, n0), rebuilt for every
-// B issue, with extents that end at the last valid element of that range,
-// so every offset stays small; the range check still zero-fills rows past
-// M and K, and chunks past N are redirected past the extent.
+// B issue, with extents that end at the last valid element of that range
+// (B: at the end of the chunk holding it), so every offset stays small; the
+// range check still zero-fills rows past M and K, and chunks past N are
+// redirected past the extent.
 template <int DT, int TM, int TN, int STAGES, bool WIDE = false>
 __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_kernel(FastArgs g) {
   static_assert((TM == 256 && STAGES == 4) || (TM == 128 && STAGES == 3), "tile variant");
@@ -504,10 +507,11 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
     const int k0 = kt * kDmaK;
     if constexpr (WIDE) {
       // Resource for rows k0 .. k0 + 31 from column n0; rows past K are past
-      // its extent (empty once k0 >= K).
+      // its extent (empty once k0 >= K).  The last row's extent is rounded
+      // up to the 8-column chunk that holds column N - 1.
       const int rows = min(kDmaK, g.K - k0);
-      const __amdgpu_buffer_rsrc_t rk =
-          make_rsrc(g.B + (int64_t)k0 * g.ldb + n0, rows > 0 ? ((rows - 1) * g.ldb + (g.N - n0)) * 2 : 0);
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc(
+          g.B + (int64_t)k0 * g.ldb + n0, rows > 0 ? ((rows - 1) * g.ldb + ((g.N - n0 + 7) & ~7)) * 2 : 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) dma16(rk, (lds_void*)(st + kABytes + (wave * 4 + i) * 1024), b_off[i]);
     } else {
@@ -2021,10 +2025,13 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
               float* C, int64_t ldc, int M, int N, int K, hipStream_t stream, bool force_generic,
               int force_shape) {
   const int64_t kLimit = (int64_t)1 << 31;
-  // The DMA kernel masks at 8-element granularity, so it also needs K and N
-  // to be multiples of 8 (or zero padding supplied by a repack).
+  // The DMA kernel masks at 8-element granularity.  A also needs K a
+  // multiple of 8 (or zero padding supplied by a repack): a chunk straddling
+  // K would pair A's row padding, possibly Inf or NaN, with zeroed B rows.
+  // B's chunk straddling N reads padding columns (in the same 16 bytes as
+  // column N - 1) that reach only C columns >= N, which are never stored.
   const bool a_ok = aligned16(A) && lda % 8 == 0 && K % 8 == 0;
-  const bool b_ok = aligned16(B) && ldb % 8 == 0 && N % 8 == 0;
+  const bool b_ok = aligned16(B) && ldb % 8 == 0;
   const int64_t lda_p = a_ok ? lda : (int64_t)round_up(K, 8);
   const int64_t ldb_p = b_ok ? ldb : (int64_t)round_up(N, 8);
   const int64_t tiles = (int64_t)((M + kTileM - 1) / kTileM) * ((N + kTileN - 1) / kTileN);

@@ -616,6 +616,50 @@ def test_wide_b_operand_over_2gib_bit_exact():
     assert np.array_equal(c.cpu().numpy(), want)
 
 
+def test_wide_b_view_with_nan_padding_columns_bit_exact():
+    """B over 2 GiB, N not a multiple of 8, B a view whose 3 padding
+    columns hold NaN: the chunk holding column N - 1 loads them, and they
+    must reach no stored element of C."""
+    import hc.gfx950 as g
+
+    m, n, ld, k = 136, 16389, 16392, 65536
+    print(f"case wide B view m={m} n={n} ldb={ld} k={k}", flush=True)
+    rng = np.random.default_rng(9)
+    ai = rng.integers(-3, 4, size=(m, k))
+    kk = torch.arange(k, device=DEV, dtype=torch.int32).view(k, 1)
+    nn = torch.arange(ld, device=DEV, dtype=torch.int32).view(1, ld)
+    full = ((kk + nn) % 5 - 2).to(torch.float16)
+    del kk, nn
+    full[:, n:] = float("nan")
+    a = torch.from_numpy(ai.astype(np.float16)).to(DEV)
+    c = g.gemm(a, full[:, :n])
+    torch.cuda.synchronize()
+    del full
+    s = np.stack([ai[:, q::5].sum(axis=1) for q in range(5)], axis=1)
+    j = np.arange(n)
+    want = sum((r - 2) * s[:, (r - j) % 5] for r in range(5)).astype(np.float32)
+    assert np.array_equal(c.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("algo", ["auto", "tiled", "tiled_256x192", "tiled_128x128", "tiled_256x64"])
+@pytest.mark.parametrize("m,n,k", [(1000, 3001, 1024), (300, 601, 8192), (4096, 129, 512)])
+def test_b_view_with_nan_padding_columns(algo, m, n, k):
+    """N not a multiple of 8 with B's rows aligned (no repack): the padding
+    columns B loads with column N - 1 hold NaN and must not reach C."""
+    import hc.gfx950 as g
+    from hc.gfx950.workloads import make_inputs
+
+    a, b = make_inputs("c2_4096_f16", seed=n + k, m=m, n=n, k=k)
+    ld = (n + 7) // 8 * 8
+    full = torch.full((k, ld), float("nan"), dtype=torch.float16, device=DEV)
+    full[:, :n] = _dev(b)
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device=DEV)
+    print(f"case B NaN padding {algo} m={m} n={n} k={k}", flush=True)
+    g.gemm(_dev(a), full[:, :n], out=out, algo=algo)
+    torch.cuda.synchronize()
+    _check(out.cpu().numpy(), oracle.gemm_c(a, b), k)
+
+
 def test_wide_a_operand_over_2gib_bit_exact():
     import hc.gfx950 as g
 
