@@ -1710,7 +1710,8 @@ double plan_cost(const TileShape& t, int splits, int num_cus, int M, int N, int 
   return cost;
 }
 
-TilePlan plan_tiles(int num_cus, int M, int N, int K, int force_shape, bool allow_split) {
+TilePlan plan_tiles(int num_cus, int M, int N, int K, int force_shape, bool allow_split,
+                    double* cost_out = nullptr) {
   TilePlan best{force_shape >= 0 ? force_shape : 0, 1};
   double best_cost = -1;
   const int forced_splits =
@@ -1732,6 +1733,7 @@ TilePlan plan_tiles(int num_cus, int M, int N, int K, int force_shape, bool allo
       }
     }
   }
+  if (cost_out) *cost_out = best_cost;
   return best;
 }
 
@@ -2140,6 +2142,56 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
   return HCG_OK;
 }
 
+// Remainder peeling (HCG_ALGO_AUTO only).  A few rows or columns past a
+// multiple of 256 can cost the tiled kernel a whole extra round of tiles
+// (4100 x 4096 x 4096: 272 tiles of 256 x 256 for 256 CUs).  When the model
+// prefers it, the tile-aligned bulk runs on the tiled kernel and the
+// remainder -- up to 128 rows, or up to 32 columns -- on the matching
+// streaming kernel, each writing its own rows or columns of C.
+struct Peel {
+  int rows = 0, cols = 0;
+};
+
+double tiled_cost(int num_cus, int M, int N, int K) {
+  double cost = 0;
+  plan_tiles(num_cus, M, N, K, -1, true, &cost);
+  return cost;
+}
+
+// A streaming launch in the tile model's units (0.73 us per 256 x 256 x 1):
+// a fixed 8 us (launch behind the tiled kernel, ramp-up, the K split's
+// reduce) plus its bytes at 5 TB/s.  Fitted so that short-K shapes
+// (4100 x 4096 x 256: 20.4 us unpeeled, 23.1 us peeled) stay unpeeled.
+double stream_units(double bytes) { return (8.0 + bytes / 5.0e6) / 0.73 * 65536.0; }
+
+Peel plan_peel(const DeviceState* st, const void* A, int64_t lda, const void* B, int64_t ldb, int M, int N,
+               int K) {
+  Peel p;
+  double best = 0.95 * tiled_cost(st->num_cus, M, N, K);  // a clear gain pays for the second launch
+  const int rm = M % 256;
+  if (M > 256 && rm > 0 && rm <= 128 &&
+      (rm <= 16 || stream_fits(static_cast<const uint16_t*>(A) + (int64_t)(M - rm) * lda, lda, B, ldb, rm, N, K))) {
+    const double c = tiled_cost(st->num_cus, M - rm, N, K) +
+                     stream_units(2.0 * K * N + 2.0 * rm * K + 4.0 * rm * N);
+    if (c < best) {
+      best = c;
+      p.rows = rm;
+    }
+  }
+  const int rn = N % 256;
+  if (N > 256 && rn > 0 && rn <= 32 &&
+      rowstream_fits(A, lda, static_cast<const uint16_t*>(B) + (N - rn), ldb, M, rn, K)) {
+    const double c = tiled_cost(st->num_cus, M, N - rn, K) +
+                     stream_units(2.0 * M * K + 2.0 * K * rn + 4.0 * M * rn);
+    if (c < best) {
+      best = c;
+      p.rows = 0;
+      p.cols = rn;
+    }
+  }
+  return p;
+}
+
 int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
               float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream_ptr) {
   if (dtype != HCG_F16 && dtype != HCG_BF16)
@@ -2201,8 +2253,23 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
     rc = run_skinny(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream);
   } else {
     const int force_shape = algo >= HCG_ALGO_TILED_256x256 ? algo - HCG_ALGO_TILED_256x256 : -1;
-    rc = run_tiled(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream,
-                   algo == HCG_ALGO_GENERIC, force_shape);
+    const Peel peel = algo == HCG_ALGO_AUTO ? plan_peel(st, A, lda, B, ldb, (int)M, (int)N, (int)K) : Peel{};
+    if (peel.rows > 0) {
+      const int mm = (int)M - peel.rows;
+      rc = run_tiled(st, dtype, A, lda, B, ldb, C, ldc, mm, (int)N, (int)K, stream, false, -1);
+      if (rc == HCG_OK)
+        rc = run_skinny(st, dtype, static_cast<const uint16_t*>(A) + (int64_t)mm * lda, lda, B, ldb,
+                        C + (int64_t)mm * ldc, ldc, peel.rows, (int)N, (int)K, stream);
+    } else if (peel.cols > 0) {
+      const int nn = (int)N - peel.cols;
+      rc = run_tiled(st, dtype, A, lda, B, ldb, C, ldc, (int)M, nn, (int)K, stream, false, -1);
+      if (rc == HCG_OK)
+        rc = run_rowstream(st, dtype, A, lda, static_cast<const uint16_t*>(B) + nn, ldb, C + nn, ldc, (int)M,
+                           peel.cols, (int)K, stream);
+    } else {
+      rc = run_tiled(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream,
+                     algo == HCG_ALGO_GENERIC, force_shape);
+    }
   }
   if (rc == HCG_OK) t_last_error.clear();
   return rc;

@@ -189,7 +189,9 @@ def gemm(a: Any, b: Any, out: Any | None = None, *, algo: str = "auto", device: 
     ``algo``: "auto" (the library picks: the streaming kernel for M <= 16,
     and up to 128 rows with 16-byte aligned rows; the narrow streaming
     kernel for N <= 32 with A's rows aligned and K a multiple of 8;
-    otherwise the LDS-tiled kernel with a modelled tile shape and K split),
+    otherwise the LDS-tiled kernel with a modelled tile shape and K split,
+    with up to 128 rows or 32 columns past a multiple of 256 peeled off to
+    a streaming kernel when that saves a round of tiles),
     "tiled", "skinny", "narrow", "generic", or a fixed tile shape
     "tiled_256x256", "tiled_256x192", "tiled_128x256", "tiled_128x128",
     "tiled_256x64" (never split along K).

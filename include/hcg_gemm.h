@@ -68,7 +68,9 @@ int hcg_init(void);
 
 /* C = A @ B, the launch of `tiled_gfx11_wmma_matmul`
  * (examples/amdgpu_gfx11_wmma_matmul.py:301-326) through
- * hc.simulator.launch (hc/simulator.py:165-186).  Picks the kernel by shape. */
+ * hc.simulator.launch (hc/simulator.py:165-186).  Picks the kernel by shape;
+ * a few rows or columns past a multiple of 256 may run on a streaming
+ * kernel beside the tiled one (two launches on the stream). */
 int hcg_gemm(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, float* C,
              int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
 

@@ -660,6 +660,49 @@ def test_b_view_with_nan_padding_columns(algo, m, n, k):
     _check(out.cpu().numpy(), oracle.gemm_c(a, b), k)
 
 
+# Remainder peeling (algo "auto"): rows or columns just past a multiple of
+# 256 run the bulk on the tiled kernel and the remainder on a streaming
+# kernel (rows: the M <= 128 one; columns: the N <= 32 one).  At K = 1024
+# the library's cost model peels all of these (4 / 15 / 100 rows, 4 / 24
+# columns); at K <= 512 it keeps them whole.
+PEEL_SHAPES = [(4100, 4096, 1024, "float16"), (4111, 4096, 1024, "bfloat16"), (4196, 4096, 1024, "float16"),
+               (4096, 4100, 1024, "bfloat16"), (4096, 4120, 1024, "float16")]
+
+
+@pytest.mark.parametrize("m,n,k,dtype", PEEL_SHAPES)
+def test_remainder_peel_against_oracle_with_guard_band(m, n, k, dtype):
+    import hc.gfx950 as g
+    from hc.gfx950.workloads import make_inputs
+
+    cfg = "c2_4096_f16" if dtype == "float16" else "c3_8192_bf16"
+    a, b = make_inputs(cfg, seed=m + 7 * n + k, m=m, n=n, k=k)
+    guard = torch.full((m + 2, n + 8), float("nan"), dtype=torch.float32, device=DEV)
+    out = guard[1 : m + 1, 4 : n + 4]
+    print(f"case peel {dtype} m={m} n={n} k={k}", flush=True)
+    g.gemm(_dev(a, dtype), _dev(b, dtype), out=out)
+    torch.cuda.synchronize()
+    host = guard.cpu().numpy()
+    _check(host[1 : m + 1, 4 : n + 4], oracle.gemm_c(a, b, _dt(dtype)), k)
+    mask = np.ones_like(host, dtype=bool)
+    mask[1 : m + 1, 4 : n + 4] = False
+    assert np.all(np.isnan(host[mask]))
+
+
+@pytest.mark.parametrize("m,n,k", [(4100, 4096, 1024), (4096, 4104, 1024), (4111, 4096, 1025)])
+def test_remainder_peel_integer_bit_exact(m, n, k):
+    """Exact sums, so the peeled and unpeeled results must agree bit for
+    bit; 4111 x 4096 x 1025 has unaligned rows of A (the bulk repacked, the
+    15 remainder rows on the register-staged kernel)."""
+    rng = np.random.default_rng(m + n + k)
+    ai = rng.integers(-4, 5, size=(m, k))
+    bi = rng.integers(-4, 5, size=(k, n))
+    a, b = ai.astype(np.float16), bi.astype(np.float16)
+    print(f"case peel integer m={m} n={n} k={k}", flush=True)
+    want = (ai.astype(np.float64) @ bi.astype(np.float64)).astype(np.float32)  # exact: |sums| <= 16400
+    assert np.array_equal(_gemm(a, b), want)
+    assert np.array_equal(_gemm(a, b, "tiled"), want)
+
+
 def test_wide_a_operand_over_2gib_bit_exact():
     import hc.gfx950 as g
 
