@@ -6,8 +6,9 @@ through the C ABI.  Graph capture: the kernels take no host-side action
 inside a launch except on a stream's first use of a workspace size (an
 allocation), so after one warm-up call on the capture stream every path --
 tiled, skinny split-K (workspace partials + reduce), tiled split-K,
-repacked ragged operands (workspace copies) and the narrow kernel (repacked
-B, split partials) -- records into a graph.  Every replay is
+repacked ragged operands (workspace copies), the narrow kernel (repacked
+B, split partials) and a peeled shape (tiled bulk + streaming remainder, two
+launches sharing the workspace) -- records into a graph.  Every replay is
 checked against the eager result, with eager work between replays.
 """
 
@@ -39,6 +40,7 @@ CASES = [
     ("ragged", 1000, 601, 333),
     ("splitk", 512, 512, 16384),
     ("narrow", 2048, 13, 4096),
+    ("peel", 4111, 4096, 1024),
 ]
 
 
