@@ -540,8 +540,9 @@ def test_numpy_bf16_is_not_accepted_and_launch_errors_surface():
 
 # Seeded random shapes, layouts and kernel choices against the oracle: every
 # path (tiled with and without a K split, repacked operands, the streaming
-# kernel at every row-block count, the register-staged skinny fallback and
-# the generic kernel) on shapes nobody picked by hand.
+# kernel at every row-block count, the narrow kernel, the register-staged
+# skinny fallback and the generic kernel) on shapes nobody picked by hand,
+# with NaN in the operands' row padding and around C.
 _RANDOM_ALGOS = ["auto", "auto", "auto", "tiled", "skinny", "generic", "tiled_128x128", "tiled_256x192"]
 
 
@@ -575,8 +576,9 @@ def test_random_shapes_and_layouts_against_oracle(i):
     cfg = "c2_4096_f16" if dtype == "float16" else "c3_8192_bf16"
     a, b = make_inputs(cfg, seed=i, m=m, n=n, k=k)
     tdt = torch.float16 if dtype == "float16" else torch.bfloat16
-    big_a = torch.zeros((m, k + pad_a), dtype=tdt, device=DEV)
-    big_b = torch.zeros((k, n + pad_b), dtype=tdt, device=DEV)
+    # row padding holds NaN: no kernel may let an element outside the views reach C
+    big_a = torch.full((m, k + pad_a), float("nan"), dtype=tdt, device=DEV)
+    big_b = torch.full((k, n + pad_b), float("nan"), dtype=tdt, device=DEV)
     va, vb = big_a[:, :k], big_b[:, :n]
     va.copy_(_dev(a, dtype))
     vb.copy_(_dev(b, dtype))
