@@ -1824,9 +1824,15 @@ int launch_stream(const StreamArgs& a, hipStream_t stream) {
   }
   HCG_HIP_CHECK(hipGetLastError());
   if (a.splits > 1) {
-    const int64_t total = (int64_t)a.M * (a.N / 4);
-    stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
-        a.ws, a.C, a.ldc, a.M, a.N, 16 * a.rblocks, a.splits, a.c_vec);
+    if (a.N % 4 == 0) {
+      const int64_t total = (int64_t)a.M * (a.N / 4);
+      stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
+          a.ws, a.C, a.ldc, a.M, a.N, 16 * a.rblocks, a.splits, a.c_vec);
+    } else {
+      const int64_t total = (int64_t)a.M * a.N;
+      skinny_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(a.ws, a.C, a.ldc, a.M, a.N,
+                                                                               16 * a.rblocks, a.splits);
+    }
     HCG_HIP_CHECK(hipGetLastError());
   }
   return HCG_OK;
@@ -1836,12 +1842,15 @@ int launch_stream(const StreamArgs& a, hipStream_t stream) {
 int stream_rblocks(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8; }
 
 // The streaming kernel masks at 8-element granularity through the buffer
-// range check: it needs aligned rows, K and N multiples of 8, and byte
-// offsets below 2^31 for every row block it reads.
+// range check: it needs aligned rows, K a multiple of 8 (a chunk straddling
+// K would pair A's row padding, possibly Inf or NaN, with zeroed B rows),
+// and byte offsets below 2^31 for every row block it reads.  N need not be a
+// multiple of 8: the chunk holding column N - 1 also loads up to 7 padding
+// columns of B, which reach only output columns >= N (never stored).
 bool stream_fits(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K) {
   const int64_t kLimit = (int64_t)1 << 31;
   return M <= 16 * kStMaxRowBlocks && aligned16(A) && lda % 8 == 0 && K % 8 == 0 && aligned16(B) &&
-         ldb % 8 == 0 && N % 8 == 0 && ((int64_t)16 * stream_rblocks(M) * lda + K) * 2 < kLimit &&
+         ldb % 8 == 0 && ((int64_t)16 * stream_rblocks(M) * lda + K) * 2 < kLimit &&
          ((int64_t)round_up(K, kStStep) * ldb + round_up(N, kStN)) * 2 < kLimit;
 }
 
@@ -1880,7 +1889,7 @@ int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const voi
   // reduce kernel.
   if (M > 16)
     return set_error(HCG_EINVAL,
-                     "the skinny kernel needs 16-byte aligned rows and K, N multiples of 8 for M > 16 "
+                     "the skinny kernel needs 16-byte aligned rows and K a multiple of 8 for M > 16 "
                      "(M=%d)", M);
   SkinnyArgs a{};
   a.A = static_cast<const uint16_t*>(A);

@@ -53,7 +53,7 @@ class Gfx950Target:
     device: GPU index for host (numpy) buffers; device tensors run where they
         live.  None = the current device.
     algo: "auto" (by shape), "tiled", "skinny" (M <= 128; above 16 rows
-        only with 16-byte aligned rows and K, N multiples of 8) or "narrow"
+        only with 16-byte aligned rows and K a multiple of 8) or "narrow"
         (N <= 32, A's rows 16-byte aligned, K a multiple of 8).
     max_group_size: HIP's workgroup limit, checked like the simulator's.
     """

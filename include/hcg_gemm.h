@@ -76,8 +76,8 @@ int hcg_gemm(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, 
 
 /* Same as hcg_gemm with an explicit kernel choice (HCG_ALGO_*).  Used by
  * tests and the benchmark to exercise each kernel; HCG_ALGO_SKINNY rejects
- * M > 128, and M > 16 with rows that are not 16-byte aligned or K, N not
- * multiples of 8, and HCG_ALGO_NARROW rejects N > 32, A's rows not 16-byte
+ * M > 128, and M > 16 with rows that are not 16-byte aligned or K not a
+ * multiple of 8, and HCG_ALGO_NARROW rejects N > 32, A's rows not 16-byte
  * aligned and K not a multiple of 8, with HCG_EINVAL. */
 int hcg_gemm_algo(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
                   float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);

@@ -556,12 +556,13 @@ def _random_case(i):
     n = int(rng.integers(1, 1600))
     k = int(rng.choice([rng.integers(1, 64), rng.integers(64, 2048), rng.integers(2048, 9000)]))
     if algo == "skinny" and m > 16:
-        # above 16 rows the skinny path needs aligned rows and K, N multiples of 8
-        n, k = max(8, n // 8 * 8), max(8, k // 8 * 8)
+        # above 16 rows the skinny path needs aligned rows and K a multiple of 8
+        k = max(8, k // 8 * 8)
     pad_a = int(rng.choice([0, 0, 1, 3, 8]))
     pad_b = int(rng.choice([0, 0, 1, 5, 8]))
     if algo == "skinny" and m > 16:
-        pad_a, pad_b = pad_a // 8 * 8, pad_b // 8 * 8
+        # aligned rows: B's row stride padded to a multiple of 8 (N itself may not be)
+        pad_a, pad_b = pad_a // 8 * 8, (-n) % 8 + pad_b // 8 * 8
     dtype = "float16" if rng.random() < 0.7 else "bfloat16"
     return algo, m, n, k, pad_a, pad_b, dtype
 
@@ -687,6 +688,34 @@ def test_remainder_peel_against_oracle_with_guard_band(m, n, k, dtype):
     _check(host[1 : m + 1, 4 : n + 4], oracle.gemm_c(a, b, _dt(dtype)), k)
     mask = np.ones_like(host, dtype=bool)
     mask[1 : m + 1, 4 : n + 4] = False
+    assert np.all(np.isnan(host[mask]))
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 8191, 8192), (100, 4099, 2048), (17, 30, 4096), (128, 1, 1024)])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_streaming_kernel_any_n_with_nan_padding(m, n, k, dtype):
+    """17..128 rows, N not a multiple of 8, B's rows padded to a multiple of
+    8 with NaN: the chunk holding column N - 1 loads padding that must
+    reach no stored element (with and without a K split; the split's
+    partials are summed one element per thread when N % 4 != 0)."""
+    import hc.gfx950 as g
+    from hc.gfx950.workloads import make_inputs
+
+    cfg = "c2_4096_f16" if dtype == "float16" else "c3_8192_bf16"
+    a, b = make_inputs(cfg, seed=m + n, m=m, n=n, k=k)
+    ld = (n + 7) // 8 * 8
+    full = torch.full((k, ld), float("nan"), dtype=torch.float16 if dtype == "float16" else torch.bfloat16,
+                      device=DEV)
+    full[:, :n] = _dev(b, dtype)
+    guard = torch.full((m + 2, n + 2), float("nan"), dtype=torch.float32, device=DEV)
+    out = guard[1 : m + 1, 1 : n + 1]
+    print(f"case stream any N {dtype} m={m} n={n} k={k}", flush=True)
+    g.gemm(_dev(a, dtype), full[:, :n], out=out, algo="skinny")
+    torch.cuda.synchronize()
+    host = guard.cpu().numpy()
+    _check(host[1 : m + 1, 1 : n + 1], oracle.gemm_c(a, b, _dt(dtype)), k)
+    mask = np.ones_like(host, dtype=bool)
+    mask[1 : m + 1, 1 : n + 1] = False
     assert np.all(np.isnan(host[mask]))
 
 
