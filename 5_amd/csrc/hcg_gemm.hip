@@ -19,20 +19,23 @@
 //     by the buffer range check, and an LDS-staged 16-byte epilogue; shapes
 //     with few tiles and a long K split K over workgroups (partials summed
 //     in a fixed order by stream_reduce_kernel).
-//   * gemm_stream_kernel -- M <= 128 with aligned operands (HBM-bound).  B
-//     streams HBM -> LDS once through a DMA ring, split over K across
+//   * gemm_stream_kernel -- M <= 128 with B's rows aligned (HBM-bound; A
+//     repacked when needed).  B streams HBM -> LDS once through a DMA ring,
+//     split over K across
 //     workgroups mapped so every XCD covers all column residues, against
 //     1, 2, 4 or 8 16-row blocks of A; the split partials are summed in a
 //     fixed order (deterministic).
 //   * gemm_generic_kernel -- fallback (plain pointers, register staging, any
 //     alignment) for unaligned operands whose byte offsets do not fit 31
 //     bits; aligned ones that large run the DMA kernel's WIDE form.
-//   * gemm_skinny_kernel -- M <= 16 with unaligned operands: B streamed with
+//   * gemm_rowstream_kernel -- N <= 32 with A's rows aligned (HBM-bound): A
+//     streams HBM -> LDS once in 256-byte row pieces, split over K.
+//   * gemm_skinny_kernel -- M <= 16 with B's rows unaligned: B streamed with
 //     128-bit loads, transposed 8x8 in registers, split over K; partial sums
 //     reduced in a fixed order.
 //   * repack_kernel -- copies operands whose rows are not 16-byte aligned
-//     (or whose K / N is not a multiple of 8) into zero-padded aligned rows
-//     for the DMA kernels.
+//     (or, for A, whose K is not a multiple of 8) into zero-padded aligned
+//     rows for the DMA kernels.
 //
 // Numerics: products of fp16/bf16 values are exact in float32 and the MFMA
 // accumulates in float32; only the order of the float32 additions differs
@@ -1842,26 +1845,36 @@ int launch_stream(const StreamArgs& a, hipStream_t stream) {
 int stream_rblocks(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8; }
 
 // The streaming kernel masks at 8-element granularity through the buffer
-// range check: it needs aligned rows, K a multiple of 8 (a chunk straddling
-// K would pair A's row padding, possibly Inf or NaN, with zeroed B rows),
-// and byte offsets below 2^31 for every row block it reads.  N need not be a
-// multiple of 8: the chunk holding column N - 1 also loads up to 7 padding
-// columns of B, which reach only output columns >= N (never stored).
+// range check.  B, the streamed operand, needs 16-byte aligned rows; N need
+// not be a multiple of 8 (the chunk holding column N - 1 also loads up to 7
+// padding columns, which reach only output columns >= N, never stored).  A
+// (at most 128 rows) is used in place when its rows are aligned and K is a
+// multiple of 8, and otherwise repacked into zero-padded rows of
+// round_up(K, 8) (a chunk straddling K would pair A's row padding, possibly
+// Inf or NaN, with zeroed B rows).  Byte offsets stay below 2^31.
+bool stream_extent_a(int64_t lda, int64_t M, int64_t K) {
+  return ((int64_t)16 * stream_rblocks(M) * lda + K) * 2 < ((int64_t)1 << 31);
+}
+bool stream_a_in_place(const void* A, int64_t lda, int64_t M, int64_t K) {
+  return aligned16(A) && lda % 8 == 0 && K % 8 == 0 && stream_extent_a(lda, M, K);
+}
 bool stream_fits(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K) {
   const int64_t kLimit = (int64_t)1 << 31;
-  return M <= 16 * kStMaxRowBlocks && aligned16(A) && lda % 8 == 0 && K % 8 == 0 && aligned16(B) &&
-         ldb % 8 == 0 && ((int64_t)16 * stream_rblocks(M) * lda + K) * 2 < kLimit &&
-         ((int64_t)round_up(K, kStStep) * ldb + round_up(N, kStN)) * 2 < kLimit;
+  return M <= 16 * kStMaxRowBlocks && aligned16(B) && ldb % 8 == 0 &&
+         ((int64_t)round_up(K, kStStep) * ldb + round_up(N, kStN)) * 2 < kLimit &&
+         (stream_a_in_place(A, lda, M, K) || stream_extent_a(round_up(K, 8), M, K));
 }
 
 int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
                float* C, int64_t ldc, int M, int N, int K, hipStream_t stream) {
   if (stream_fits(A, lda, B, ldb, M, N, K)) {
+    const bool a_in_place = stream_a_in_place(A, lda, M, K);
+    const int64_t lda_use = a_in_place ? lda : (int64_t)round_up(K, 8);
     StreamArgs a{};
     a.A = static_cast<const uint16_t*>(A);
     a.B = static_cast<const uint16_t*>(B);
     a.C = C;
-    a.lda = (int)lda;
+    a.lda = (int)lda_use;
     a.ldb = (int)ldb;
     a.ldc = ldc;
     a.M = M;
@@ -1872,16 +1885,28 @@ int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const voi
     a.kchunk = ((ksteps + a.splits - 1) / a.splits) * kStStep;
     a.splits = (K + a.kchunk - 1) / a.kchunk;  // drop empty trailing splits
     a.rblocks = stream_rblocks(M);
-    a.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda + K) * 2, 16);
+    a.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda_use + K) * 2, 16);
     a.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * ldb + N) * 2, 16);
     a.c_vec = aligned16(C) && ldc % 4 == 0;
     a.ws = nullptr;
-    if (a.splits > 1) {
+    // Workspace: A repacked (when it cannot be used in place), then the
+    // split partials.
+    const size_t a_sz = a_in_place ? 0 : round_up((size_t)M * lda_use * 2, 256);
+    const size_t p_sz = a.splits > 1 ? (size_t)a.splits * 16 * a.rblocks * (size_t)N * sizeof(float) : 0;
+    if (a_sz + p_sz > 0) {
       void* ws = nullptr;
-      const int rc = stream_workspace(st, stream, (size_t)a.splits * 16 * a.rblocks * (size_t)N * sizeof(float),
-                                      &ws);
+      const int rc = stream_workspace(st, stream, a_sz + p_sz, &ws);
       if (rc != HCG_OK) return rc;
-      a.ws = static_cast<float*>(ws);
+      if (!a_in_place) {
+        uint16_t* a_p = static_cast<uint16_t*>(ws);
+        const RepackJob ja{a.A, lda, M, K, a_p, (int)lda_use, (int64_t)M * (lda_use / 8)};
+        const RepackJob jb{};
+        const int64_t per_block = (int64_t)256 * kRepackPer;
+        repack_kernel<<<(unsigned)((ja.chunks + per_block - 1) / per_block), 256, 0, stream>>>(ja, jb);
+        HCG_HIP_CHECK(hipGetLastError());
+        a.A = a_p;
+      }
+      if (a.splits > 1) a.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + a_sz);
     }
     return dtype == HCG_F16 ? launch_stream<HCG_F16>(a, stream) : launch_stream<HCG_BF16>(a, stream);
   }
@@ -1889,7 +1914,7 @@ int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const voi
   // reduce kernel.
   if (M > 16)
     return set_error(HCG_EINVAL,
-                     "the skinny kernel needs 16-byte aligned rows and K a multiple of 8 for M > 16 "
+                     "the skinny kernel needs B's rows 16-byte aligned (ldb a multiple of 8) for M > 16 "
                      "(M=%d)", M);
   SkinnyArgs a{};
   a.A = static_cast<const uint16_t*>(A);

@@ -259,15 +259,39 @@ def test_skinny_row_blocks_integer_bit_exact(m, dtype):
 
 def test_skinny_rows_need_aligned_operands_or_fall_back_to_tiles():
     """Above 16 rows the skinny path is the streaming kernel only: an
-    explicit request with unaligned rows is a LaunchError, while auto
-    takes the tiled kernel for the same operands."""
+    explicit request with B's rows unaligned is a LaunchError, while auto
+    takes the tiled kernel for the same operands; A's rows need not be
+    aligned (A is repacked)."""
     from hc import LaunchError
     from hc.gfx950.workloads import make_inputs
 
     a, b = make_inputs("c4_skinny_f16", seed=3, m=40, n=1001, k=333)
-    with pytest.raises(LaunchError, match="aligned rows"):
+    with pytest.raises(LaunchError, match="B's rows 16-byte aligned"):
         _gemm(a, b, "skinny")
     _check(_gemm(a, b, "auto"), oracle.gemm_c(a, b), 333)
+    a, b = make_inputs("c4_skinny_f16", seed=4, m=40, n=1000, k=333)
+    _check(_gemm(a, b, "skinny"), oracle.gemm_c(a, b), 333)
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 8192, 8191), (64, 2048, 4095), (128, 1000, 1001), (5, 4096, 2049)])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_streaming_kernel_with_a_repacked(m, n, k, dtype):
+    """K not a multiple of 8 (A's rows unaligned): A is repacked into
+    zero-padded rows and B still streams through the DMA kernel; A's row
+    padding holds NaN."""
+    import hc.gfx950 as g
+    from hc.gfx950.workloads import make_inputs
+
+    cfg = "c4_skinny_f16" if dtype == "float16" else "c3_8192_bf16"
+    a, b = make_inputs(cfg, seed=m + k, m=m, n=n, k=k)
+    tdt = torch.float16 if dtype == "float16" else torch.bfloat16
+    big_a = torch.full((m, k + 3), float("nan"), dtype=tdt, device=DEV)
+    big_a[:, :k] = _dev(a, dtype)
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device=DEV)
+    print(f"case stream repacked A {dtype} m={m} n={n} k={k}", flush=True)
+    g.gemm(big_a[:, :k], _dev(b, dtype), out=out, algo="skinny")
+    torch.cuda.synchronize()
+    _check(out.cpu().numpy(), oracle.gemm_c(a, b, _dt(dtype)), k)
 
 
 # Few output tiles and a long K: the tiled kernel splits K over several
