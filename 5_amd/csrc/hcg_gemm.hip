@@ -974,7 +974,7 @@ struct StreamArgs {
   const uint16_t* B;
   float* C;
   float* ws;      // [splits][16 * row blocks][N] partial sums (splits > 1)
-  int lda, ldb;   // elements, multiples of 8
+  int lda, ldb;   // elements; lda a multiple of 8, ldb too unless B is register-staged
   int64_t ldc;
   int M, N, K;
   int kchunk;     // rows per split, multiple of kStStep
@@ -1051,7 +1051,16 @@ __device__ __forceinline__ unsigned char* st_a() {
 // distinct 16-byte bank groups.
 __device__ __forceinline__ int sta_swz(int row, int c) { return c ^ ((row >> 2) & 3); }
 
-template <int DT, int R>
+// UB (B's rows not 16-byte aligned, so no DMA for B): each lane fetches the
+// two aligned 16-byte blocks around its B chunk kStStages - 1 stages ahead
+// into a register set of its own, and writes the chunk (shift_join of the
+// two) just before that stage's barrier to the LDS bytes the DMA would have
+// filled.  Every lane issues two loads per chunk (the wait counts double the
+// B part): chunks past N or rows past the split's K range read B's first
+// block and are cleared, and a second block past B's last byte is replaced
+// by the first (its bytes reach only columns >= N).  Needs B 2-byte aligned
+// and (K - 1) * ldb + N >= 8.
+template <int DT, int R, bool UB = false>
 __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
   static_assert(R >= 1 && R <= kStMaxRowBlocks, "row blocks");
   constexpr int NB = kStN;
@@ -1114,19 +1123,61 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
     a_off[i] = (row * g.lda + a_c * 8) * 2;
   }
 
+  // UB: register sets of the stages in flight (the two aligned 16-byte
+  // blocks around each chunk), and per chunk its byte offset in the first
+  // block, or -1 for a cleared chunk.
+  u32x4 breg[UB ? kStStages : 1][kDmaPerWave][2];
+  int bsh[UB ? kStStages : 1][kDmaPerWave];
+  u32x4 areg[UB ? kStStages : 1][kAPer];
+  bool alive[UB ? kStStages : 1][kAPer];
+  const uintptr_t b_base = reinterpret_cast<uintptr_t>(g.B);
+  const uintptr_t b_end = b_base + ((uintptr_t)(g.K - 1) * g.ldb + g.N) * 2;  // one past B's last byte
+
   auto issue = [&](auto sc, int step) {
     constexpr int S = decltype(sc)::value;
     const int k0 = kbeg + step * kStStep;
+    if constexpr (UB) {
 #pragma unroll
-    for (int i = 0; i < kDmaPerWave; ++i) {
-      const int off = dma_offset(k0 + b_row[i] < kend, b_off[i] + k0 * g.ldb * 2);
-      dma16(rsrc_b, (lds_void*)(st_b<S>() + (wave * kDmaPerWave + i) * 1024), off);
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        const int row = k0 + (wave * kDmaPerWave + i) * kRowsPerDma + lane / (NB / 8);
+        const int col = n0 + b_chunk_swz(row - k0, lane % (NB / 8)) * 8;
+        const bool live = row < kend && col < g.N;
+        // Selects, not branches: a branch around the address math lets the
+        // compiler's wait insertion fall back to waiting for every load.
+        const int row_c = live ? row : 0, col_c = live ? col : 0;
+        const uintptr_t p = b_base + ((uintptr_t)((uint64_t)(uint32_t)row_c * (uint32_t)g.ldb) + (uint32_t)col_c) * 2;
+        const uintptr_t q = p & ~(uintptr_t)15;
+        // The second block is read only when it holds a byte of B (a 16-byte
+        // block never crosses a page); otherwise the first is read again.
+        const uintptr_t q1 = q + 16 < b_end ? q + 16 : q;
+        bsh[S][i] = live ? (int)(p - q) : -1;
+        // Global (not generic) pointers: a flat load also counts on lgkmcnt,
+        // so the wait for LDS writes before each barrier would drain it.
+        using gvec = const __attribute__((address_space(1))) u32x4;
+        breg[S][i][0] = *reinterpret_cast<gvec*>(q);
+        breg[S][i][1] = *reinterpret_cast<gvec*>(q1);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        const int off = dma_offset(k0 + b_row[i] < kend, b_off[i] + k0 * g.ldb * 2);
+        dma16(rsrc_b, (lds_void*)(st_b<S>() + (wave * kDmaPerWave + i) * 1024), off);
+      }
     }
 #pragma unroll
     for (int i = 0; i < kAPer; ++i) {
       if (wave + 4 * i < R) {
-        const int off = dma_offset(a_ok[i] && k0 + a_c * 8 < kend, a_off[i] + k0 * 2);
-        dma16(rsrc_a, (lds_void*)(st_a<R, S>() + (wave + 4 * i) * kStABytes), off);
+        const bool live = a_ok[i] && k0 + a_c * 8 < kend;
+        if constexpr (UB) {
+          // A through registers too: with an LDS DMA in flight the compiler
+          // waits for it (and so for every older load) before LDS reads.
+          using gvec = const __attribute__((address_space(1))) u32x4;
+          const int off = live ? (a_off[i] + k0 * 2) / 2 : 0;
+          areg[S][i] = *reinterpret_cast<gvec*>(reinterpret_cast<uintptr_t>(g.A + off));
+          alive[S][i] = live;
+        } else {
+          dma16(rsrc_a, (lds_void*)(st_a<R, S>() + (wave + 4 * i) * kStABytes), dma_offset(live, a_off[i] + k0 * 2));
+        }
       }
     }
   };
@@ -1178,12 +1229,27 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
   constexpr int kLater = kStStages - 2;
   auto step_fn = [&](auto sc, int step) {
     constexpr int S = decltype(sc)::value;
+    constexpr int kBLoads = UB ? 2 * kDmaPerWave : kDmaPerWave;  // B memory instructions per stage
     if constexpr (R % 4 == 0) {
-      wait_vmcnt<(kDmaPerWave + R / 4) * kLater>();
+      wait_vmcnt<(kBLoads + R / 4) * kLater>();
     } else if (wave < R % 4) {
-      wait_vmcnt<(kDmaPerWave + R / 4 + 1) * kLater>();
+      wait_vmcnt<(kBLoads + R / 4 + 1) * kLater>();
     } else {
-      wait_vmcnt<(kDmaPerWave + R / 4) * kLater>();
+      wait_vmcnt<(kBLoads + R / 4) * kLater>();
+    }
+    if constexpr (UB) {
+      // This wave's B chunks of the stage have landed in registers.
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        const int sh = bsh[S][i];
+        const u32x4 v = sh < 0 ? u32x4{0, 0, 0, 0} : shift_join(breg[S][i][0], breg[S][i][1], sh);
+        *reinterpret_cast<u32x4*>(st_b<S>() + (wave * kDmaPerWave + i) * 1024 + lane * 16) = v;
+      }
+#pragma unroll
+      for (int i = 0; i < kAPer; ++i)
+        if (wave + 4 * i < R)
+          *reinterpret_cast<u32x4*>(st_a<R, S>() + (wave + 4 * i) * kStABytes + lane * 16) =
+              alive[S][i] ? areg[S][i] : u32x4{0, 0, 0, 0};
     }
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
@@ -1812,17 +1878,17 @@ int stream_splits(const DeviceState* st, int nblocks, int K) {
   return splits;
 }
 
-template <int DT>
+template <int DT, bool UB>
 int launch_stream(const StreamArgs& a, hipStream_t stream) {
   // Column blocks padded to a multiple of 8 per split (see the workgroup
   // mapping in gemm_stream_kernel); padding workgroups exit at once.
   const int nblocks = (a.N + kStN - 1) / kStN;
   const dim3 grid((unsigned)(round_up(nblocks, 8) * a.splits));
   switch (a.rblocks) {
-    case 1: gemm_stream_kernel<DT, 1><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 2: gemm_stream_kernel<DT, 2><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 4: gemm_stream_kernel<DT, 4><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 8: gemm_stream_kernel<DT, 8><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 1: gemm_stream_kernel<DT, 1, UB><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 2: gemm_stream_kernel<DT, 2, UB><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 4: gemm_stream_kernel<DT, 4, UB><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 8: gemm_stream_kernel<DT, 8, UB><<<grid, dim3(256), 0, stream>>>(a); break;
     default: return set_error(HCG_EINVAL, "internal: %d row blocks", a.rblocks);
   }
   HCG_HIP_CHECK(hipGetLastError());
@@ -1858,10 +1924,16 @@ bool stream_extent_a(int64_t lda, int64_t M, int64_t K) {
 bool stream_a_in_place(const void* A, int64_t lda, int64_t M, int64_t K) {
   return aligned16(A) && lda % 8 == 0 && K % 8 == 0 && stream_extent_a(lda, M, K);
 }
+bool stream_b_dma(const void* B, int64_t ldb, int64_t N, int64_t K) {
+  return aligned16(B) && ldb % 8 == 0 &&
+         ((int64_t)round_up(K, kStStep) * ldb + round_up(N, kStN)) * 2 < ((int64_t)1 << 31);
+}
+// B that the DMA cannot take (rows not 16-byte aligned, or offsets past
+// 2^31) is register-staged: 16-byte loads at any 2-byte alignment, all
+// inside B's extent, which must then hold at least 8 elements.
 bool stream_fits(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K) {
-  const int64_t kLimit = (int64_t)1 << 31;
-  return M <= 16 * kStMaxRowBlocks && aligned16(B) && ldb % 8 == 0 &&
-         ((int64_t)round_up(K, kStStep) * ldb + round_up(N, kStN)) * 2 < kLimit &&
+  return M <= 16 * kStMaxRowBlocks && ldb < ((int64_t)1 << 31) &&
+         (stream_b_dma(B, ldb, N, K) || (K - 1) * ldb + N >= 8) &&
          (stream_a_in_place(A, lda, M, K) || stream_extent_a(round_up(K, 8), M, K));
 }
 
@@ -1886,7 +1958,8 @@ int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const voi
     a.splits = (K + a.kchunk - 1) / a.kchunk;  // drop empty trailing splits
     a.rblocks = stream_rblocks(M);
     a.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda_use + K) * 2, 16);
-    a.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * ldb + N) * 2, 16);
+    // (register-staged B reads through plain pointers: no extent)
+    a.b_bytes = stream_b_dma(B, ldb, N, K) ? (int)round_up((size_t)(((int64_t)K - 1) * ldb + N) * 2, 16) : 0;
     a.c_vec = aligned16(C) && ldc % 4 == 0;
     a.ws = nullptr;
     // Workspace: A repacked (when it cannot be used in place), then the
@@ -1908,13 +1981,16 @@ int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const voi
       }
       if (a.splits > 1) a.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + a_sz);
     }
-    return dtype == HCG_F16 ? launch_stream<HCG_F16>(a, stream) : launch_stream<HCG_BF16>(a, stream);
+    if (stream_b_dma(B, ldb, N, K))
+      return dtype == HCG_F16 ? launch_stream<HCG_F16, false>(a, stream) : launch_stream<HCG_BF16, false>(a, stream);
+    return dtype == HCG_F16 ? launch_stream<HCG_F16, true>(a, stream) : launch_stream<HCG_BF16, true>(a, stream);
   }
   // Fallback for unaligned operands (M <= 16): register-staged kernel +
   // reduce kernel.
   if (M > 16)
     return set_error(HCG_EINVAL,
-                     "the skinny kernel needs B's rows 16-byte aligned (ldb a multiple of 8) for M > 16 "
+                     "the skinny kernel cannot take this layout for M > 16 (B under 8 elements, or offsets "
+                     "of A past 2^31) "
                      "(M=%d)", M);
   SkinnyArgs a{};
   a.A = static_cast<const uint16_t*>(A);

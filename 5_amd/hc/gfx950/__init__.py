@@ -52,9 +52,9 @@ class Gfx950Target:
 
     device: GPU index for host (numpy) buffers; device tensors run where they
         live.  None = the current device.
-    algo: "auto" (by shape), "tiled", "skinny" (M <= 128; above 16 rows
-        only with 16-byte aligned rows and K a multiple of 8) or "narrow"
-        (N <= 32, A's rows 16-byte aligned, K a multiple of 8).
+    algo: "auto" (by shape), "tiled", "skinny" (M <= 128, any layout
+        whose B holds at least 8 elements) or "narrow" (N <= 32, A's rows
+        16-byte aligned, K a multiple of 8).
     max_group_size: HIP's workgroup limit, checked like the simulator's.
     """
 
@@ -186,8 +186,9 @@ def gemm(a: Any, b: Any, out: Any | None = None, *, algo: str = "auto", device: 
     computed, and copied back into ``out`` (created if None); the call then
     returns after the result is on the host.
 
-    ``algo``: "auto" (the library picks: the streaming kernel for M <= 16,
-    and up to 128 rows with 16-byte aligned rows; the narrow streaming
+    ``algo``: "auto" (the library picks: the streaming kernel for M <= 128,
+    B by DMA when its rows are 16-byte aligned and through registers
+    otherwise; the narrow streaming
     kernel for N <= 32 with A's rows aligned and K a multiple of 8;
     otherwise the LDS-tiled kernel with a modelled tile shape and K split,
     with up to 128 rows or 32 columns past a multiple of 256 peeled off to

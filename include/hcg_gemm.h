@@ -48,7 +48,7 @@ extern "C" {
 /* Kernel selection for hcg_gemm_algo. */
 #define HCG_ALGO_AUTO 0
 #define HCG_ALGO_TILED 1  /* LDS-tiled MFMA kernel, tile shape and K split picked by shape (compute-bound) */
-#define HCG_ALGO_SKINNY 2 /* split-K streaming kernel for M <= 128 (HBM-bound shapes) */
+#define HCG_ALGO_SKINNY 2 /* split-K streaming kernel for M <= 128 (HBM-bound shapes; any layout) */
 #define HCG_ALGO_GENERIC 3 /* pointer-based tiled kernel: any alignment and size (fallback) */
 /* The LDS-tiled kernel with a fixed output tile shape (rows x columns), never split along K. */
 #define HCG_ALGO_TILED_256x256 4
@@ -76,8 +76,8 @@ int hcg_gemm(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, 
 
 /* Same as hcg_gemm with an explicit kernel choice (HCG_ALGO_*).  Used by
  * tests and the benchmark to exercise each kernel; HCG_ALGO_SKINNY rejects
- * M > 128, and M > 16 with rows that are not 16-byte aligned or K not a
- * multiple of 8, and HCG_ALGO_NARROW rejects N > 32, A's rows not 16-byte
+ * M > 128, and M > 16 with a B of fewer than 8 elements (or K past 2^23),
+ * and HCG_ALGO_NARROW rejects N > 32, A's rows not 16-byte
  * aligned and K not a multiple of 8, with HCG_EINVAL. */
 int hcg_gemm_algo(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
                   float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);

@@ -257,20 +257,45 @@ def test_skinny_row_blocks_integer_bit_exact(m, dtype):
     assert np.array_equal(_gemm(a, b, "skinny", dtype), (ai @ bi).astype(np.float32))
 
 
-def test_skinny_rows_need_aligned_operands_or_fall_back_to_tiles():
-    """Above 16 rows the skinny path is the streaming kernel only: an
-    explicit request with B's rows unaligned is a LaunchError, while auto
-    takes the tiled kernel for the same operands; A's rows need not be
-    aligned (A is repacked)."""
+def test_skinny_rows_take_any_layout_but_a_tiny_b():
+    """Above 16 rows the skinny path is the streaming kernel only: A is
+    repacked when its rows are not aligned, B's unaligned rows are
+    register-staged; a B of fewer than 8 elements is a LaunchError for an
+    explicit request, while auto takes the tiled kernel."""
     from hc import LaunchError
     from hc.gfx950.workloads import make_inputs
 
-    a, b = make_inputs("c4_skinny_f16", seed=3, m=40, n=1001, k=333)
-    with pytest.raises(LaunchError, match="B's rows 16-byte aligned"):
+    for seed, (m, n, k) in enumerate([(40, 1001, 333), (40, 1000, 333), (17, 9, 7)]):
+        a, b = make_inputs("c4_skinny_f16", seed=3 + seed, m=m, n=n, k=k)
+        _check(_gemm(a, b, "skinny"), oracle.gemm_c(a, b), k)
+    a, b = make_inputs("c4_skinny_f16", seed=9, m=40, n=5, k=1)
+    with pytest.raises(LaunchError, match="B under 8 elements"):
         _gemm(a, b, "skinny")
-    _check(_gemm(a, b, "auto"), oracle.gemm_c(a, b), 333)
-    a, b = make_inputs("c4_skinny_f16", seed=4, m=40, n=1000, k=333)
-    _check(_gemm(a, b, "skinny"), oracle.gemm_c(a, b), 333)
+    _check(_gemm(a, b, "auto"), oracle.gemm_c(a, b), 1)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 8191, 8192), (16, 8191, 8191), (17, 50257, 1024), (64, 1001, 4096),
+                                   (128, 333, 2049), (5, 7, 9), (100, 8, 1), (16, 4099, 16384)])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_streaming_kernel_register_staged_b(m, n, k, dtype):
+    """B's rows not 16-byte aligned (tight, odd N): register-staged B in the
+    streaming kernel, including the chunk that ends at B's last element
+    (loaded as the 16 bytes ending there and shifted), C in a NaN guard band."""
+    import hc.gfx950 as g
+    from hc.gfx950.workloads import make_inputs
+
+    cfg = "c4_skinny_f16" if dtype == "float16" else "c3_8192_bf16"
+    a, b = make_inputs(cfg, seed=m + n + k, m=m, n=n, k=k)
+    guard = torch.full((m + 2, n + 2), float("nan"), dtype=torch.float32, device=DEV)
+    out = guard[1 : m + 1, 1 : n + 1]
+    print(f"case stream register-staged B {dtype} m={m} n={n} k={k}", flush=True)
+    g.gemm(_dev(a, dtype), _dev(b, dtype), out=out, algo="skinny")
+    torch.cuda.synchronize()
+    host = guard.cpu().numpy()
+    _check(host[1 : m + 1, 1 : n + 1], oracle.gemm_c(a, b, _dt(dtype)), k)
+    mask = np.ones_like(host, dtype=bool)
+    mask[1 : m + 1, 1 : n + 1] = False
+    assert np.all(np.isnan(host[mask]))
 
 
 @pytest.mark.parametrize("m,n,k", [(16, 8192, 8191), (64, 2048, 4095), (128, 1000, 1001), (5, 4096, 2049)])
