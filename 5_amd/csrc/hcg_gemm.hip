@@ -1343,7 +1343,7 @@ struct RowStreamArgs {
   const uint16_t* B;
   float* C;
   float* ws;      // [splits][M][N] partial sums (splits > 1)
-  int lda, ldb;   // elements, multiples of 8
+  int lda, ldb;   // elements; multiples of 8 (lda not when A is register-staged)
   int64_t ldc;
   int M, N, K;
   int kchunk;     // K per split, multiple of kRsStep
@@ -1381,13 +1381,23 @@ __device__ __forceinline__ unsigned char* rs_b() {
   else return g_rsb5;
 }
 
-template <int DT, int NB>
+// UA (A's rows not 16-byte aligned or K not a multiple of 8, so no DMA for
+// A): each lane loads the two aligned 16-byte blocks around its A chunk
+// kRsStages - 1 stages ahead into registers, and just before the stage's
+// barrier writes the funnel-shifted chunk, elements at k >= K cleared (the
+// row padding may hold Inf or NaN), to the LDS bytes the DMA would fill.  B
+// (16-byte aligned rows, repacked when needed) comes through registers too:
+// with an LDS DMA in flight the compiler waits for it, and so for every
+// older load, before LDS reads.  A second block past A's last byte is
+// replaced by the first (its bytes are k >= K, cleared).
+template <int DT, int NB, bool UA = false>
 __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
   static_assert(NB == 16 || NB == 32, "column block");
   constexpr int kChunksB = NB / 8;               // 16-byte chunks per staged B row
   constexpr int kRowsPerBDma = 64 / kChunksB;    // B rows per DMA instruction
   constexpr int kBDmaPerWave = kRsStep / kRowsPerBDma / 4;
   constexpr int kDmaPerWave = 4 + kBDmaPerWave;  // 4 A instructions (16 rows x 256 B)
+  constexpr int kLoadsPerWave = UA ? 8 + kBDmaPerWave : kDmaPerWave;  // memory instructions per stage
   constexpr int kBlocks = NB / 16;               // MFMA column blocks
 
   const int tid = threadIdx.x;
@@ -1413,7 +1423,7 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
     const int row = 16 * wave + 4 * i + (lane >> 4);
     const int c = (lane & 15) ^ (row & 15);
     a_col[i] = c * 8;
-    a_off[i] = ((m0 + row) * g.lda + c * 8) * 2;
+    a_off[i] = UA ? 0 : ((m0 + row) * g.lda + c * 8) * 2;  // (UA reads through 64-bit pointers)
   }
   int b_off[kBDmaPerWave], b_row[kBDmaPerWave];
 #pragma unroll
@@ -1422,6 +1432,23 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
     const int cb = lane % kChunksB;
     b_row[i] = cb * 8 < g.N ? kr : 0x3fffffff;
     b_off[i] = (kr * g.ldb + cb * 8) * 2;
+  }
+  // UA: register sets of the stages in flight; per A chunk its byte offset
+  // in the first block (-1: cleared) and its elements below K.
+  using gvec = const __attribute__((address_space(1))) u32x4;
+  u32x4 areg[UA ? kRsStages : 1][4][2];
+  int ash[UA ? kRsStages : 1][4], avld[UA ? kRsStages : 1][4];
+  u32x4 breg[UA ? kRsStages : 1][kBDmaPerWave];
+  bool bok[UA ? kRsStages : 1][kBDmaPerWave];
+  const uintptr_t a_base = reinterpret_cast<uintptr_t>(g.A), b_base = reinterpret_cast<uintptr_t>(g.B);
+  const uintptr_t a_end = a_base + ((uintptr_t)(g.M - 1) * g.lda + g.K) * 2;  // one past A's last byte
+  uintptr_t a_rowp[4];
+  bool a_rowok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = m0 + 16 * wave + 4 * i + (lane >> 4);
+    a_rowok[i] = row < g.M;
+    a_rowp[i] = a_base + (uintptr_t)(a_rowok[i] ? row : 0) * (uintptr_t)g.lda * 2;
   }
 
   // Row block rb walks its run of K starting at step rb % nsteps (wrapping):
@@ -1436,14 +1463,35 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
     int s = step + rot;
     if (s >= nsteps) s -= nsteps;
     const int k0 = step < nsteps ? kbeg + s * kRsStep : kend;
+    if constexpr (UA) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma16(rsrc_a, (lds_void*)(rs_a<S>() + (16 * wave + 4 * i) * 256),
-            dma_offset(k0 + a_col[i] < kend, a_off[i] + k0 * 2));
+      for (int i = 0; i < 4; ++i) {
+        const int kc = k0 + a_col[i];  // the chunk's first k
+        const bool live = a_rowok[i] && kc < kend;
+        const uintptr_t p = live ? a_rowp[i] + (uintptr_t)kc * 2 : a_base;
+        const uintptr_t q = p & ~(uintptr_t)15;
+        const uintptr_t q1 = q + 16 < a_end ? q + 16 : q;
+        ash[S][i] = live ? (int)(p - q) : -1;
+        avld[S][i] = min(8, g.K - kc);
+        areg[S][i][0] = *reinterpret_cast<gvec*>(q);
+        areg[S][i][1] = *reinterpret_cast<gvec*>(q1);
+      }
 #pragma unroll
-    for (int i = 0; i < kBDmaPerWave; ++i)
-      dma16(rsrc_b, (lds_void*)(rs_b<S>() + (wave * kBDmaPerWave + i) * 1024),
-            dma_offset(k0 + b_row[i] < kend, b_off[i] + k0 * g.ldb * 2));
+      for (int i = 0; i < kBDmaPerWave; ++i) {
+        const bool live = k0 + b_row[i] < kend;
+        bok[S][i] = live;
+        breg[S][i] = *reinterpret_cast<gvec*>(live ? b_base + (uintptr_t)(b_off[i] + k0 * g.ldb * 2) : b_base);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        dma16(rsrc_a, (lds_void*)(rs_a<S>() + (16 * wave + 4 * i) * 256),
+              dma_offset(k0 + a_col[i] < kend, a_off[i] + k0 * 2));
+#pragma unroll
+      for (int i = 0; i < kBDmaPerWave; ++i)
+        dma16(rsrc_b, (lds_void*)(rs_b<S>() + (wave * kBDmaPerWave + i) * 1024),
+              dma_offset(k0 + b_row[i] < kend, b_off[i] + k0 * g.ldb * 2));
+    }
   };
 
   // Fragment addresses.  A, k step j: row 16w + l%16, chunk 4j + l/16.  B,
@@ -1492,7 +1540,23 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
   constexpr int kLater = kRsStages - 2;
   auto step_fn = [&](auto sc, int step) {
     constexpr int S = decltype(sc)::value;
-    wait_vmcnt<kDmaPerWave * kLater>();
+    wait_vmcnt<kLoadsPerWave * kLater>();
+    if constexpr (UA) {
+      // This wave's chunks of the stage have landed in registers.
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int sh = ash[S][i], nv = avld[S][i];
+        u32x4 v = sh < 0 ? u32x4{0, 0, 0, 0} : shift_join(areg[S][i][0], areg[S][i][1], sh);
+#pragma unroll
+        for (int w = 0; w < 4; ++w)  // elements 2w, 2w + 1 (k >= K cleared)
+          v[w] = 2 * w + 1 < nv ? v[w] : (2 * w < nv ? v[w] & 0xffffu : 0u);
+        *reinterpret_cast<u32x4*>(rs_a<S>() + (16 * wave + 4 * i) * 256 + lane * 16) = v;
+      }
+#pragma unroll
+      for (int i = 0; i < kBDmaPerWave; ++i)
+        *reinterpret_cast<u32x4*>(rs_b<S>() + (wave * kBDmaPerWave + i) * 1024 + lane * 16) =
+            bok[S][i] ? breg[S][i] : u32x4{0, 0, 0, 0};
+    }
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -2023,13 +2087,16 @@ int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const voi
 // The narrow-N streaming kernel: N <= 32, aligned rows, K a multiple of 8,
 // byte offsets below 2^31.
 // B's rows need not be aligned: B (at most 32 columns) is repacked when they
-// are not.
+// are not.  A goes by DMA when its rows are 16-byte aligned, K is a multiple
+// of 8 and its offsets stay below 2^31, and through registers otherwise.
+bool rowstream_a_dma(const void* A, int64_t lda, int64_t M, int64_t K) {
+  return aligned16(A) && lda % 8 == 0 && K % 8 == 0 &&
+         ((int64_t)round_up(M, kRsRows) * lda + round_up(K, kRsStep)) * 2 < ((int64_t)1 << 31);
+}
 bool rowstream_fits(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K) {
-  const int64_t kLimit = (int64_t)1 << 31;
   const int64_t ldb_use = aligned16(B) && ldb % 8 == 0 ? ldb : round_up(N, 8);
-  return N <= 32 && aligned16(A) && lda % 8 == 0 && K % 8 == 0 &&
-         ((int64_t)round_up(M, kRsRows) * lda + round_up(K, kRsStep)) * 2 < kLimit &&
-         ((int64_t)round_up(K, kRsStep) * ldb_use + 32) * 2 < kLimit;
+  return N <= 32 && lda < ((int64_t)1 << 31) &&
+         ((int64_t)round_up(K, kRsStep) * ldb_use + 32) * 2 < ((int64_t)1 << 31);
 }
 
 int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
@@ -2077,16 +2144,21 @@ int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const 
     }
     if (a.splits > 1) a.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + b_sz);
   }
-  a.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda + K) * 2, 16);
+  const bool a_dma = rowstream_a_dma(A, lda, M, K);
+  a.a_bytes = a_dma ? (int)round_up((size_t)(((int64_t)M - 1) * lda + K) * 2, 16) : 0;
   a.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * a.ldb + N) * 2, 16);
   const dim3 grid((unsigned)(nrb * a.splits));
   const bool wide = N > 16;
-  if (dtype == HCG_F16) {
-    if (wide) gemm_rowstream_kernel<HCG_F16, 32><<<grid, dim3(256), 0, stream>>>(a);
-    else gemm_rowstream_kernel<HCG_F16, 16><<<grid, dim3(256), 0, stream>>>(a);
-  } else {
-    if (wide) gemm_rowstream_kernel<HCG_BF16, 32><<<grid, dim3(256), 0, stream>>>(a);
-    else gemm_rowstream_kernel<HCG_BF16, 16><<<grid, dim3(256), 0, stream>>>(a);
+  const int variant = (dtype == HCG_F16 ? 0 : 4) + (wide ? 2 : 0) + (a_dma ? 0 : 1);
+  switch (variant) {
+    case 0: gemm_rowstream_kernel<HCG_F16, 16, false><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 1: gemm_rowstream_kernel<HCG_F16, 16, true><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 2: gemm_rowstream_kernel<HCG_F16, 32, false><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 3: gemm_rowstream_kernel<HCG_F16, 32, true><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 4: gemm_rowstream_kernel<HCG_BF16, 16, false><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 5: gemm_rowstream_kernel<HCG_BF16, 16, true><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 6: gemm_rowstream_kernel<HCG_BF16, 32, false><<<grid, dim3(256), 0, stream>>>(a); break;
+    default: gemm_rowstream_kernel<HCG_BF16, 32, true><<<grid, dim3(256), 0, stream>>>(a); break;
   }
   HCG_HIP_CHECK(hipGetLastError());
   if (a.splits > 1) {
@@ -2352,7 +2424,7 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
                                           (algo == HCG_ALGO_AUTO && rowstream_fits(A, lda, B, ldb, M, N, K)));
   if (algo == HCG_ALGO_NARROW && !rowstream_fits(A, lda, B, ldb, M, N, K))
     return set_error(HCG_EINVAL,
-                     "the narrow kernel needs N <= 32, 16-byte aligned rows of A and K a multiple of 8 "
+                     "the narrow kernel needs N <= 32 (and offsets of B below 2^31) "
                      "(M=%lld N=%lld K=%lld)", (long long)M, (long long)N, (long long)K);
   // Workspaces stay valid while ws_mutex is held (see stream_workspace), so
   // the lock covers the launches too; a launch only enqueues work.

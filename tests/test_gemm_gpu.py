@@ -422,9 +422,44 @@ def test_narrow_kernel_rejects_what_it_cannot_run():
     a, b = make_inputs("c2_4096_f16", seed=1, m=100, n=40, k=256)
     with pytest.raises(LaunchError, match="narrow kernel needs N <= 32"):
         _gemm(a, b, "narrow")
-    a, b = make_inputs("c2_4096_f16", seed=1, m=100, n=8, k=257)
-    with pytest.raises(LaunchError, match="K a multiple of 8"):
-        _gemm(a, b, "narrow")
+
+
+@pytest.mark.parametrize("m,n,k", [(100, 8, 257), (16384, 8, 16383), (4096, 13, 8191), (3000, 32, 4095),
+                                   (777, 1, 9), (65, 17, 1), (2049, 24, 130)])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_narrow_kernel_register_staged_a(m, n, k, dtype):
+    """A's rows not 16-byte aligned (K odd in a tight A, plus NaN row
+    padding beyond K in a view): A goes through registers in the narrow
+    kernel and elements at k >= K are cleared before they meet B."""
+    import hc.gfx950 as g
+    from hc.gfx950.workloads import make_inputs
+
+    cfg = "c2_4096_f16" if dtype == "float16" else "c3_8192_bf16"
+    a, b = make_inputs(cfg, seed=m + n + k, m=m, n=n, k=k)
+    want = oracle.gemm_c(a, b, _dt(dtype))
+    print(f"case narrow register-staged A {dtype} m={m} n={n} k={k}", flush=True)
+    _check(_gemm(a, b, "narrow", dtype), want, k)
+    tdt = torch.float16 if dtype == "float16" else torch.bfloat16
+    big_a = torch.full((m, k + 5), float("nan"), dtype=tdt, device=DEV)
+    big_a[:, :k] = _dev(a, dtype)
+    guard = torch.full((m + 2, n + 2), float("nan"), dtype=torch.float32, device=DEV)
+    out = guard[1 : m + 1, 1 : n + 1]
+    g.gemm(big_a[:, :k], _dev(b, dtype), out=out, algo="narrow")
+    torch.cuda.synchronize()
+    host = guard.cpu().numpy()
+    _check(host[1 : m + 1, 1 : n + 1], want, k)
+    mask = np.ones_like(host, dtype=bool)
+    mask[1 : m + 1, 1 : n + 1] = False
+    assert np.all(np.isnan(host[mask]))
+
+
+def test_narrow_kernel_register_staged_a_integer_bit_exact():
+    rng = np.random.default_rng(21)
+    ai = rng.integers(-4, 5, size=(5000, 4095))
+    bi = rng.integers(-4, 5, size=(4095, 11))
+    want = (ai.astype(np.float64) @ bi.astype(np.float64)).astype(np.float32)
+    got = _gemm(ai.astype(np.float16), bi.astype(np.float16), "narrow")
+    assert np.array_equal(got, want)
 
 
 def test_skinny_repeated_launches_alternating_shapes():
