@@ -28,7 +28,7 @@
 //   * gemm_generic_kernel -- fallback (plain pointers, register staging, any
 //     alignment) for unaligned operands whose byte offsets do not fit 31
 //     bits; aligned ones that large run the DMA kernel's WIDE form.
-//   * gemm_rowstream_kernel -- N <= 32 with A's rows aligned (HBM-bound): A
+//   * gemm_rowstream_kernel -- N <= 64, any layout (HBM-bound): A
 //     streams HBM -> LDS once in 256-byte row pieces, split over K.
 //   * gemm_skinny_kernel -- M <= 16 with B's rows unaligned: B streamed with
 //     128-bit loads, transposed 8x8 in registers, split over K; partial sums
@@ -1317,7 +1317,7 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
 // Narrow-N streaming kernel: A through LDS by DMA in 256-byte row pieces
 // ---------------------------------------------------------------------------
 //
-// For N <= 32 the product is bound by reading A (M x K) once, and the
+// For N <= 64 the product is bound by reading A (M x K) once, and the
 // tiled kernel's 64-byte row pieces per 32-wide K step stream poorly.  Here
 // a workgroup (256 threads) takes 64 rows of A over a run of K (split-K
 // when the row blocks alone do not fill the chip); wave w owns rows
@@ -1334,9 +1334,11 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
 
 constexpr int kRsRows = 64;
 constexpr int kRsStep = 128;
-constexpr int kRsStages = 6;
+constexpr int kRsStages = 6;            // NB <= 32 (24 KB per stage)
+constexpr int kRs64Stages = 5;          // NB = 64 (32 KB per stage: 160 KB, all of a CU's LDS)
 constexpr int kRsABytes = kRsRows * kRsStep * 2;  // 16 KB
 constexpr int kRsBBytes = kRsStep * 32 * 2;       // 8 KB (NB <= 32)
+constexpr int kRsB64Bytes = kRsStep * 64 * 2;     // 16 KB (NB = 64)
 
 struct RowStreamArgs {
   const uint16_t* A;
@@ -1362,23 +1364,46 @@ HCG_RS_STAGE(4)
 HCG_RS_STAGE(5)
 #undef HCG_RS_STAGE
 
-template <int S>
+// NB = 64: A and B of a stage in one object (a kernel allocates only the
+// objects it names).
+#define HCG_RS64_STAGE(i) \
+  __shared__ __attribute__((aligned(1024))) unsigned char g_rsc##i[kRsABytes + kRsB64Bytes];
+HCG_RS64_STAGE(0)
+HCG_RS64_STAGE(1)
+HCG_RS64_STAGE(2)
+HCG_RS64_STAGE(3)
+HCG_RS64_STAGE(4)
+#undef HCG_RS64_STAGE
+
+template <int NB, int S>
 __device__ __forceinline__ unsigned char* rs_a() {
-  if constexpr (S == 0) return g_rsa0;
-  else if constexpr (S == 1) return g_rsa1;
-  else if constexpr (S == 2) return g_rsa2;
-  else if constexpr (S == 3) return g_rsa3;
-  else if constexpr (S == 4) return g_rsa4;
-  else return g_rsa5;
+  if constexpr (NB == 64) {
+    if constexpr (S == 0) return g_rsc0;
+    else if constexpr (S == 1) return g_rsc1;
+    else if constexpr (S == 2) return g_rsc2;
+    else if constexpr (S == 3) return g_rsc3;
+    else return g_rsc4;
+  } else {
+    if constexpr (S == 0) return g_rsa0;
+    else if constexpr (S == 1) return g_rsa1;
+    else if constexpr (S == 2) return g_rsa2;
+    else if constexpr (S == 3) return g_rsa3;
+    else if constexpr (S == 4) return g_rsa4;
+    else return g_rsa5;
+  }
 }
-template <int S>
+template <int NB, int S>
 __device__ __forceinline__ unsigned char* rs_b() {
-  if constexpr (S == 0) return g_rsb0;
-  else if constexpr (S == 1) return g_rsb1;
-  else if constexpr (S == 2) return g_rsb2;
-  else if constexpr (S == 3) return g_rsb3;
-  else if constexpr (S == 4) return g_rsb4;
-  else return g_rsb5;
+  if constexpr (NB == 64) {
+    return rs_a<NB, S>() + kRsABytes;
+  } else {
+    if constexpr (S == 0) return g_rsb0;
+    else if constexpr (S == 1) return g_rsb1;
+    else if constexpr (S == 2) return g_rsb2;
+    else if constexpr (S == 3) return g_rsb3;
+    else if constexpr (S == 4) return g_rsb4;
+    else return g_rsb5;
+  }
 }
 
 // UA (A's rows not 16-byte aligned or K not a multiple of 8, so no DMA for
@@ -1392,7 +1417,8 @@ __device__ __forceinline__ unsigned char* rs_b() {
 // replaced by the first (its bytes are k >= K, cleared).
 template <int DT, int NB, bool UA = false>
 __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
-  static_assert(NB == 16 || NB == 32, "column block");
+  static_assert(NB == 16 || NB == 32 || NB == 64, "column block");
+  constexpr int STAGES = NB == 64 ? kRs64Stages : kRsStages;
   constexpr int kChunksB = NB / 8;               // 16-byte chunks per staged B row
   constexpr int kRowsPerBDma = 64 / kChunksB;    // B rows per DMA instruction
   constexpr int kBDmaPerWave = kRsStep / kRowsPerBDma / 4;
@@ -1436,10 +1462,10 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
   // UA: register sets of the stages in flight; per A chunk its byte offset
   // in the first block (-1: cleared) and its elements below K.
   using gvec = const __attribute__((address_space(1))) u32x4;
-  u32x4 areg[UA ? kRsStages : 1][4][2];
-  int ash[UA ? kRsStages : 1][4], avld[UA ? kRsStages : 1][4];
-  u32x4 breg[UA ? kRsStages : 1][kBDmaPerWave];
-  bool bok[UA ? kRsStages : 1][kBDmaPerWave];
+  u32x4 areg[UA ? STAGES : 1][4][2];
+  int ash[UA ? STAGES : 1][4], avld[UA ? STAGES : 1][4];
+  u32x4 breg[UA ? STAGES : 1][kBDmaPerWave];
+  bool bok[UA ? STAGES : 1][kBDmaPerWave];
   const uintptr_t a_base = reinterpret_cast<uintptr_t>(g.A), b_base = reinterpret_cast<uintptr_t>(g.B);
   const uintptr_t a_end = a_base + ((uintptr_t)(g.M - 1) * g.lda + g.K) * 2;  // one past A's last byte
   uintptr_t a_rowp[4];
@@ -1485,11 +1511,11 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        dma16(rsrc_a, (lds_void*)(rs_a<S>() + (16 * wave + 4 * i) * 256),
+        dma16(rsrc_a, (lds_void*)(rs_a<NB, S>() + (16 * wave + 4 * i) * 256),
               dma_offset(k0 + a_col[i] < kend, a_off[i] + k0 * 2));
 #pragma unroll
       for (int i = 0; i < kBDmaPerWave; ++i)
-        dma16(rsrc_b, (lds_void*)(rs_b<S>() + (wave * kBDmaPerWave + i) * 1024),
+        dma16(rsrc_b, (lds_void*)(rs_b<NB, S>() + (wave * kBDmaPerWave + i) * 1024),
               dma_offset(k0 + b_row[i] < kend, b_off[i] + k0 * g.ldb * 2));
     }
   };
@@ -1520,13 +1546,13 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
     constexpr int S = decltype(sc)::value;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const u32x4 af = *reinterpret_cast<const u32x4*>(rs_a<S>() + fa[j]);
+      const u32x4 af = *reinterpret_cast<const u32x4*>(rs_a<NB, S>() + fa[j]);
 #pragma unroll
       for (int cb = 0; cb < kBlocks; ++cb) {
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(rs_b<S>() + fb[j][cb][0]));
+            (__attribute__((address_space(3))) s16x4*)(rs_b<NB, S>() + fb[j][cb][0]));
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(rs_b<S>() + fb[j][cb][1]));
+            (__attribute__((address_space(3))) s16x4*)(rs_b<NB, S>() + fb[j][cb][1]));
         const uint64_t l64 = __builtin_bit_cast(uint64_t, lo), h64 = __builtin_bit_cast(uint64_t, hi);
         const u32x4 bf = u32x4{(uint32_t)l64, (uint32_t)(l64 >> 32), (uint32_t)h64, (uint32_t)(h64 >> 32)};
         acc[cb] = mfma16x16x32<DT>(af, bf, acc[cb]);
@@ -1535,9 +1561,9 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
   };
 
   // Same step structure as the skinny streaming kernel: wait for stage S
-  // (kRsStages - 2 newer stages may be in flight), barrier, refill the
+  // (STAGES - 2 newer stages may be in flight), barrier, refill the
   // stage freed one step earlier, multiply.
-  constexpr int kLater = kRsStages - 2;
+  constexpr int kLater = STAGES - 2;
   auto step_fn = [&](auto sc, int step) {
     constexpr int S = decltype(sc)::value;
     wait_vmcnt<kLoadsPerWave * kLater>();
@@ -1550,17 +1576,17 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
 #pragma unroll
         for (int w = 0; w < 4; ++w)  // elements 2w, 2w + 1 (k >= K cleared)
           v[w] = 2 * w + 1 < nv ? v[w] : (2 * w < nv ? v[w] & 0xffffu : 0u);
-        *reinterpret_cast<u32x4*>(rs_a<S>() + (16 * wave + 4 * i) * 256 + lane * 16) = v;
+        *reinterpret_cast<u32x4*>(rs_a<NB, S>() + (16 * wave + 4 * i) * 256 + lane * 16) = v;
       }
 #pragma unroll
       for (int i = 0; i < kBDmaPerWave; ++i)
-        *reinterpret_cast<u32x4*>(rs_b<S>() + (wave * kBDmaPerWave + i) * 1024 + lane * 16) =
+        *reinterpret_cast<u32x4*>(rs_b<NB, S>() + (wave * kBDmaPerWave + i) * 1024 + lane * 16) =
             bok[S][i] ? breg[S][i] : u32x4{0, 0, 0, 0};
     }
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    issue(StageC<(S + kRsStages - 1) % kRsStages>{}, step + kRsStages - 1);
+    issue(StageC<(S + STAGES - 1) % STAGES>{}, step + STAGES - 1);
     compute(sc);
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -1569,22 +1595,23 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
   issue(StageC<1>{}, 1);
   issue(StageC<2>{}, 2);
   issue(StageC<3>{}, 3);
-  issue(StageC<4>{}, 4);
+  if constexpr (STAGES == 6) issue(StageC<4 % STAGES>{}, 4);
 
   int step = 0;
-  for (; step + kRsStages <= nsteps; step += kRsStages) {
+  for (; step + STAGES <= nsteps; step += STAGES) {
     step_fn(StageC<0>{}, step);
     step_fn(StageC<1>{}, step + 1);
     step_fn(StageC<2>{}, step + 2);
     step_fn(StageC<3>{}, step + 3);
     step_fn(StageC<4>{}, step + 4);
-    step_fn(StageC<5>{}, step + 5);
+    if constexpr (STAGES == 6) step_fn(StageC<5 % STAGES>{}, step + 5);
   }
   if (step < nsteps) step_fn(StageC<0>{}, step++);
   if (step < nsteps) step_fn(StageC<1>{}, step++);
   if (step < nsteps) step_fn(StageC<2>{}, step++);
   if (step < nsteps) step_fn(StageC<3>{}, step++);
-  if (step < nsteps) step_fn(StageC<4>{}, step++);
+  if constexpr (STAGES == 6)
+    if (step < nsteps) step_fn(StageC<4 % STAGES>{}, step++);
   wait_vmcnt<0>();  // no DMA may still be writing LDS at exit
 
   // 16x16 accumulator layout: register r of lane l holds row 4*(l/16) + r,
@@ -2084,7 +2111,7 @@ int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const voi
                           : launch_skinny<HCG_BF16>(a, vec_a, vec_b, stream);
 }
 
-// The narrow-N streaming kernel: N <= 32, aligned rows, K a multiple of 8,
+// The narrow-N streaming kernel: N <= 64, A by DMA or through registers,
 // byte offsets below 2^31.
 // B's rows need not be aligned: B (at most 32 columns) is repacked when they
 // are not.  A goes by DMA when its rows are 16-byte aligned, K is a multiple
@@ -2095,8 +2122,16 @@ bool rowstream_a_dma(const void* A, int64_t lda, int64_t M, int64_t K) {
 }
 bool rowstream_fits(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K) {
   const int64_t ldb_use = aligned16(B) && ldb % 8 == 0 ? ldb : round_up(N, 8);
-  return N <= 32 && lda < ((int64_t)1 << 31) &&
-         ((int64_t)round_up(K, kRsStep) * ldb_use + 32) * 2 < ((int64_t)1 << 31);
+  return N <= 64 && lda < ((int64_t)1 << 31) &&
+         ((int64_t)round_up(K, kRsStep) * ldb_use + 64) * 2 < ((int64_t)1 << 31);
+}
+
+template <int DT, int NB>
+void launch_rowstream(const RowStreamArgs& a, bool ua, dim3 grid, hipStream_t stream) {
+  if (ua)
+    gemm_rowstream_kernel<DT, NB, true><<<grid, dim3(256), 0, stream>>>(a);
+  else
+    gemm_rowstream_kernel<DT, NB, false><<<grid, dim3(256), 0, stream>>>(a);
 }
 
 int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
@@ -2148,17 +2183,15 @@ int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const 
   a.a_bytes = a_dma ? (int)round_up((size_t)(((int64_t)M - 1) * lda + K) * 2, 16) : 0;
   a.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * a.ldb + N) * 2, 16);
   const dim3 grid((unsigned)(nrb * a.splits));
-  const bool wide = N > 16;
-  const int variant = (dtype == HCG_F16 ? 0 : 4) + (wide ? 2 : 0) + (a_dma ? 0 : 1);
-  switch (variant) {
-    case 0: gemm_rowstream_kernel<HCG_F16, 16, false><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 1: gemm_rowstream_kernel<HCG_F16, 16, true><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 2: gemm_rowstream_kernel<HCG_F16, 32, false><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 3: gemm_rowstream_kernel<HCG_F16, 32, true><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 4: gemm_rowstream_kernel<HCG_BF16, 16, false><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 5: gemm_rowstream_kernel<HCG_BF16, 16, true><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 6: gemm_rowstream_kernel<HCG_BF16, 32, false><<<grid, dim3(256), 0, stream>>>(a); break;
-    default: gemm_rowstream_kernel<HCG_BF16, 32, true><<<grid, dim3(256), 0, stream>>>(a); break;
+  const int nb = N <= 16 ? 16 : N <= 32 ? 32 : 64;
+  if (dtype == HCG_F16) {
+    if (nb == 16) launch_rowstream<HCG_F16, 16>(a, !a_dma, grid, stream);
+    else if (nb == 32) launch_rowstream<HCG_F16, 32>(a, !a_dma, grid, stream);
+    else launch_rowstream<HCG_F16, 64>(a, !a_dma, grid, stream);
+  } else {
+    if (nb == 16) launch_rowstream<HCG_BF16, 16>(a, !a_dma, grid, stream);
+    else if (nb == 32) launch_rowstream<HCG_BF16, 32>(a, !a_dma, grid, stream);
+    else launch_rowstream<HCG_BF16, 64>(a, !a_dma, grid, stream);
   }
   HCG_HIP_CHECK(hipGetLastError());
   if (a.splits > 1) {
@@ -2418,13 +2451,13 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
   // N/128 workgroups of the tiled kernel.
   const bool use_skinny = algo == HCG_ALGO_SKINNY ||
                           (algo == HCG_ALGO_AUTO && (M <= 16 || stream_fits(A, lda, B, ldb, M, N, K)));
-  // N <= 32 (and more than 16 rows) is HBM-bound on A: stream A in 256-byte
+  // N <= 64 (and more than 128 rows) is HBM-bound on A: stream A in 256-byte
   // row pieces.
   const bool use_narrow = !use_skinny && (algo == HCG_ALGO_NARROW ||
                                           (algo == HCG_ALGO_AUTO && rowstream_fits(A, lda, B, ldb, M, N, K)));
   if (algo == HCG_ALGO_NARROW && !rowstream_fits(A, lda, B, ldb, M, N, K))
     return set_error(HCG_EINVAL,
-                     "the narrow kernel needs N <= 32 (and offsets of B below 2^31) "
+                     "the narrow kernel needs N <= 64 (and offsets of B below 2^31) "
                      "(M=%lld N=%lld K=%lld)", (long long)M, (long long)N, (long long)K);
   // Workspaces stay valid while ws_mutex is held (see stream_workspace), so
   // the lock covers the launches too; a launch only enqueues work.

@@ -53,7 +53,7 @@ class Gfx950Target:
     device: GPU index for host (numpy) buffers; device tensors run where they
         live.  None = the current device.
     algo: "auto" (by shape), "tiled", "skinny" (M <= 128, any layout
-        whose B holds at least 8 elements) or "narrow" (N <= 32, any
+        whose B holds at least 8 elements) or "narrow" (N <= 64, any
         layout).
     max_group_size: HIP's workgroup limit, checked like the simulator's.
     """
@@ -189,7 +189,7 @@ def gemm(a: Any, b: Any, out: Any | None = None, *, algo: str = "auto", device: 
     ``algo``: "auto" (the library picks: the streaming kernel for M <= 128,
     B by DMA when its rows are 16-byte aligned and through registers
     otherwise; the narrow streaming
-    kernel for N <= 32, A by DMA or through registers likewise;
+    kernel for N <= 64, A by DMA or through registers likewise;
     otherwise the LDS-tiled kernel with a modelled tile shape and K split,
     with up to 128 rows or 32 columns past a multiple of 256 peeled off to
     a streaming kernel when that saves a round of tiles),

@@ -56,7 +56,7 @@ extern "C" {
 #define HCG_ALGO_TILED_128x256 6
 #define HCG_ALGO_TILED_128x128 7
 #define HCG_ALGO_TILED_256x64 8
-/* Streaming kernel for N <= 32 (A streamed once in 256-byte row pieces, K split to fill the
+/* Streaming kernel for N <= 64 (A streamed once in 256-byte row pieces, K split to fill the
  * chip; HBM-bound shapes).  Any layout: A by DMA when its rows are 16-byte aligned and K is a
  * multiple of 8, through registers otherwise; B repacked when its rows are not aligned. */
 #define HCG_ALGO_NARROW 9
@@ -77,7 +77,7 @@ int hcg_gemm(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, 
 /* Same as hcg_gemm with an explicit kernel choice (HCG_ALGO_*).  Used by
  * tests and the benchmark to exercise each kernel; HCG_ALGO_SKINNY rejects
  * M > 128, and M > 16 with a B of fewer than 8 elements (or K past 2^23),
- * and HCG_ALGO_NARROW rejects N > 32, with HCG_EINVAL. */
+ * and HCG_ALGO_NARROW rejects N > 64, with HCG_EINVAL. */
 int hcg_gemm_algo(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
                   float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
 

@@ -419,8 +419,8 @@ def test_narrow_kernel_rejects_what_it_cannot_run():
     from hc import LaunchError
     from hc.gfx950.workloads import make_inputs
 
-    a, b = make_inputs("c2_4096_f16", seed=1, m=100, n=40, k=256)
-    with pytest.raises(LaunchError, match="narrow kernel needs N <= 32"):
+    a, b = make_inputs("c2_4096_f16", seed=1, m=100, n=65, k=256)
+    with pytest.raises(LaunchError, match="narrow kernel needs N <= 64"):
         _gemm(a, b, "narrow")
 
 
@@ -448,6 +448,30 @@ def test_narrow_kernel_register_staged_a(m, n, k, dtype):
     torch.cuda.synchronize()
     host = guard.cpu().numpy()
     _check(host[1 : m + 1, 1 : n + 1], want, k)
+    mask = np.ones_like(host, dtype=bool)
+    mask[1 : m + 1, 1 : n + 1] = False
+    assert np.all(np.isnan(host[mask]))
+
+
+@pytest.mark.parametrize("m,n,k", [(1000, 48, 4096), (4096, 64, 8192), (333, 40, 520), (2049, 63, 130),
+                                   (16384, 64, 16384), (129, 33, 4095), (5000, 57, 777)])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_narrow_kernel_64_columns(m, n, k, dtype):
+    """33..64 columns: the narrow kernel's 64-column form (5-stage ring, A
+    and B of a stage in one 32 KB object), A by DMA or through registers
+    (odd K), C in a NaN guard band."""
+    import hc.gfx950 as g
+    from hc.gfx950.workloads import make_inputs
+
+    cfg = "c2_4096_f16" if dtype == "float16" else "c3_8192_bf16"
+    a, b = make_inputs(cfg, seed=m + 3 * n + k, m=m, n=n, k=k)
+    guard = torch.full((m + 2, n + 2), float("nan"), dtype=torch.float32, device=DEV)
+    out = guard[1 : m + 1, 1 : n + 1]
+    print(f"case narrow 64 {dtype} m={m} n={n} k={k}", flush=True)
+    g.gemm(_dev(a, dtype), _dev(b, dtype), out=out, algo="narrow")
+    torch.cuda.synchronize()
+    host = guard.cpu().numpy()
+    _check(host[1 : m + 1, 1 : n + 1], oracle.gemm_c(a, b, _dt(dtype)), k)
     mask = np.ones_like(host, dtype=bool)
     mask[1 : m + 1, 1 : n + 1] = False
     assert np.all(np.isnan(host[mask]))
