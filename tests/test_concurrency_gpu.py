@@ -7,8 +7,10 @@ inside a launch except on a stream's first use of a workspace size (an
 allocation), so after one warm-up call on the capture stream every path --
 tiled, skinny split-K (workspace partials + reduce), tiled split-K,
 repacked ragged operands (workspace copies), the narrow kernel (repacked
-B, split partials) and a peeled shape (tiled bulk + streaming remainder, two
-launches sharing the workspace) -- records into a graph.  Every replay is
+B, split partials), a peeled shape (tiled bulk + streaming remainder, two
+launches sharing the workspace) and the register-staged streaming forms
+(unaligned B rows; unaligned A rows in the narrow kernel) -- records into a
+graph.  Every replay is
 checked against the eager result, with eager work between replays.
 """
 
@@ -41,13 +43,16 @@ CASES = [
     ("splitk", 512, 512, 16384),
     ("narrow", 2048, 13, 4096),
     ("peel", 4111, 4096, 1024),
+    ("staged_b", 16, 8191, 4096),
+    ("staged_a", 4096, 40, 4095),
 ]
 
 
 def _inputs(name, m, n, k, seed):
     from hc.gfx950.workloads import make_inputs
 
-    return make_inputs("c4_skinny_f16" if name == "skinny" else "c2_4096_f16", seed=seed, m=m, n=n, k=k)
+    cfg = "c4_skinny_f16" if name in ("skinny", "staged_b") else "c2_4096_f16"
+    return make_inputs(cfg, seed=seed, m=m, n=n, k=k)
 
 
 def test_two_host_threads_each_with_a_stream():
