@@ -1415,10 +1415,15 @@ __device__ __forceinline__ unsigned char* rs_b() {
 // with an LDS DMA in flight the compiler waits for it, and so for every
 // older load, before LDS reads.  A second block past A's last byte is
 // replaced by the first (its bytes are k >= K, cleared).
-template <int DT, int NB, bool UA = false>
+template <int DT, int NB, bool UA = false, int ST = 0>
 __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
   static_assert(NB == 16 || NB == 32 || NB == 64, "column block");
-  constexpr int STAGES = NB == 64 ? kRs64Stages : kRsStages;
+  // ST = 3 (NB <= 32, register-staged A): a 72 KB ring, so two workgroups
+  // share a CU -- twice the waves to cover the register path's latency
+  // (65536 x 13 x 4095 fp16: 155 -> 110 us; by DMA the 6-stage ring stays
+  // ahead, 125 against 135 us at 65536 x 8 x 4096).
+  constexpr int STAGES = ST ? ST : (NB == 64 ? kRs64Stages : kRsStages);
+  static_assert(STAGES >= 3 && STAGES <= 6 && (NB < 64 || STAGES <= kRs64Stages), "stages");
   constexpr int kChunksB = NB / 8;               // 16-byte chunks per staged B row
   constexpr int kRowsPerBDma = 64 / kChunksB;    // B rows per DMA instruction
   constexpr int kBDmaPerWave = kRsStep / kRowsPerBDma / 4;
@@ -1593,24 +1598,26 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
 
   issue(StageC<0>{}, 0);
   issue(StageC<1>{}, 1);
-  issue(StageC<2>{}, 2);
-  issue(StageC<3>{}, 3);
-  if constexpr (STAGES == 6) issue(StageC<4 % STAGES>{}, 4);
+  if constexpr (STAGES > 3) issue(StageC<2 % STAGES>{}, 2);
+  if constexpr (STAGES > 4) issue(StageC<3 % STAGES>{}, 3);
+  if constexpr (STAGES > 5) issue(StageC<4 % STAGES>{}, 4);
 
   int step = 0;
   for (; step + STAGES <= nsteps; step += STAGES) {
     step_fn(StageC<0>{}, step);
     step_fn(StageC<1>{}, step + 1);
     step_fn(StageC<2>{}, step + 2);
-    step_fn(StageC<3>{}, step + 3);
-    step_fn(StageC<4>{}, step + 4);
-    if constexpr (STAGES == 6) step_fn(StageC<5 % STAGES>{}, step + 5);
+    if constexpr (STAGES > 3) step_fn(StageC<3 % STAGES>{}, step + 3);
+    if constexpr (STAGES > 4) step_fn(StageC<4 % STAGES>{}, step + 4);
+    if constexpr (STAGES > 5) step_fn(StageC<5 % STAGES>{}, step + 5);
   }
   if (step < nsteps) step_fn(StageC<0>{}, step++);
   if (step < nsteps) step_fn(StageC<1>{}, step++);
-  if (step < nsteps) step_fn(StageC<2>{}, step++);
-  if (step < nsteps) step_fn(StageC<3>{}, step++);
-  if constexpr (STAGES == 6)
+  if constexpr (STAGES > 3)
+    if (step < nsteps) step_fn(StageC<2 % STAGES>{}, step++);
+  if constexpr (STAGES > 4)
+    if (step < nsteps) step_fn(StageC<3 % STAGES>{}, step++);
+  if constexpr (STAGES > 5)
     if (step < nsteps) step_fn(StageC<4 % STAGES>{}, step++);
   wait_vmcnt<0>();  // no DMA may still be writing LDS at exit
 
@@ -2127,7 +2134,16 @@ bool rowstream_fits(const void* A, int64_t lda, const void* B, int64_t ldb, int6
 }
 
 template <int DT, int NB>
-void launch_rowstream(const RowStreamArgs& a, bool ua, dim3 grid, hipStream_t stream) {
+void launch_rowstream(const RowStreamArgs& a, bool ua, bool short_ring, dim3 grid, hipStream_t stream) {
+  if constexpr (NB <= 32) {
+    if (short_ring) {
+      if (ua)
+        gemm_rowstream_kernel<DT, NB, true, 3><<<grid, dim3(256), 0, stream>>>(a);
+      else
+        gemm_rowstream_kernel<DT, NB, false, 3><<<grid, dim3(256), 0, stream>>>(a);
+      return;
+    }
+  }
   if (ua)
     gemm_rowstream_kernel<DT, NB, true><<<grid, dim3(256), 0, stream>>>(a);
   else
@@ -2146,11 +2162,15 @@ int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const 
   a.M = M;
   a.N = N;
   a.K = K;
-  // Row blocks, then K splits until the workgroups cover the CUs (each
-  // split at least 4 stages of 128 k).
+  // Row blocks, then K splits until the workgroups cover the CUs -- twice
+  // over for register-staged A, whose 3-stage ring fits two workgroups per
+  // CU when N <= 32 (each split at least 4 stages of 128 k).
+  const bool a_dma = rowstream_a_dma(A, lda, M, K);
+  const bool short_ring = !a_dma && N <= 32;
   const int nrb = (M + kRsRows - 1) / kRsRows;
   const int ksteps = (K + kRsStep - 1) / kRsStep;
-  int splits = (st->num_cus + nrb - 1) / nrb;
+  const int target = short_ring ? 2 * st->num_cus : st->num_cus;
+  int splits = (target + nrb - 1) / nrb;
   const int max_by_k = ksteps / 4 > 0 ? ksteps / 4 : 1;
   if (splits > max_by_k) splits = max_by_k;
   if (splits > 16) splits = 16;
@@ -2179,19 +2199,18 @@ int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const 
     }
     if (a.splits > 1) a.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + b_sz);
   }
-  const bool a_dma = rowstream_a_dma(A, lda, M, K);
   a.a_bytes = a_dma ? (int)round_up((size_t)(((int64_t)M - 1) * lda + K) * 2, 16) : 0;
   a.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * a.ldb + N) * 2, 16);
   const dim3 grid((unsigned)(nrb * a.splits));
   const int nb = N <= 16 ? 16 : N <= 32 ? 32 : 64;
   if (dtype == HCG_F16) {
-    if (nb == 16) launch_rowstream<HCG_F16, 16>(a, !a_dma, grid, stream);
-    else if (nb == 32) launch_rowstream<HCG_F16, 32>(a, !a_dma, grid, stream);
-    else launch_rowstream<HCG_F16, 64>(a, !a_dma, grid, stream);
+    if (nb == 16) launch_rowstream<HCG_F16, 16>(a, !a_dma, short_ring, grid, stream);
+    else if (nb == 32) launch_rowstream<HCG_F16, 32>(a, !a_dma, short_ring, grid, stream);
+    else launch_rowstream<HCG_F16, 64>(a, !a_dma, short_ring, grid, stream);
   } else {
-    if (nb == 16) launch_rowstream<HCG_BF16, 16>(a, !a_dma, grid, stream);
-    else if (nb == 32) launch_rowstream<HCG_BF16, 32>(a, !a_dma, grid, stream);
-    else launch_rowstream<HCG_BF16, 64>(a, !a_dma, grid, stream);
+    if (nb == 16) launch_rowstream<HCG_BF16, 16>(a, !a_dma, short_ring, grid, stream);
+    else if (nb == 32) launch_rowstream<HCG_BF16, 32>(a, !a_dma, short_ring, grid, stream);
+    else launch_rowstream<HCG_BF16, 64>(a, !a_dma, short_ring, grid, stream);
   }
   HCG_HIP_CHECK(hipGetLastError());
   if (a.splits > 1) {
