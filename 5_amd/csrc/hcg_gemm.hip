@@ -2385,7 +2385,7 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
 // multiple of 256 can cost the tiled kernel a whole extra round of tiles
 // (4100 x 4096 x 4096: 272 tiles of 256 x 256 for 256 CUs).  When the model
 // prefers it, the tile-aligned bulk runs on the tiled kernel and the
-// remainder -- up to 128 rows, or up to 32 columns -- on the matching
+// remainder -- up to 128 rows, or up to 64 columns -- on the matching
 // streaming kernel, each writing its own rows or columns of C.
 struct Peel {
   int rows = 0, cols = 0;
@@ -2418,7 +2418,7 @@ Peel plan_peel(const DeviceState* st, const void* A, int64_t lda, const void* B,
     }
   }
   const int rn = N % 256;
-  if (N > 256 && rn > 0 && rn <= 32 &&
+  if (N > 256 && rn > 0 && rn <= 64 &&
       rowstream_fits(A, lda, static_cast<const uint16_t*>(B) + (N - rn), ldb, M, rn, K)) {
     const double c = tiled_cost(st->num_cus, M, N - rn, K) +
                      stream_units(2.0 * M * K + 2.0 * K * rn + 4.0 * M * rn);

@@ -191,7 +191,7 @@ def gemm(a: Any, b: Any, out: Any | None = None, *, algo: str = "auto", device: 
     otherwise; the narrow streaming
     kernel for N <= 64, A by DMA or through registers likewise;
     otherwise the LDS-tiled kernel with a modelled tile shape and K split,
-    with up to 128 rows or 32 columns past a multiple of 256 peeled off to
+    with up to 128 rows or 64 columns past a multiple of 256 peeled off to
     a streaming kernel when that saves a round of tiles),
     "tiled", "skinny", "narrow", "generic", or a fixed tile shape
     "tiled_256x256", "tiled_256x192", "tiled_128x256", "tiled_128x128",

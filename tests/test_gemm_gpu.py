@@ -773,11 +773,11 @@ def test_b_view_with_nan_padding_columns(algo, m, n, k):
 
 # Remainder peeling (algo "auto"): rows or columns just past a multiple of
 # 256 run the bulk on the tiled kernel and the remainder on a streaming
-# kernel (rows: the M <= 128 one; columns: the N <= 32 one).  At K = 1024
-# the library's cost model peels all of these (4 / 15 / 100 rows, 4 / 24
+# kernel (rows: the M <= 128 one; columns: the N <= 64 one).  At K = 1024
+# the library's cost model peels all of these (4 / 15 / 100 rows, 4 / 24 / 48
 # columns); at K <= 512 it keeps them whole.
 PEEL_SHAPES = [(4100, 4096, 1024, "float16"), (4111, 4096, 1024, "bfloat16"), (4196, 4096, 1024, "float16"),
-               (4096, 4100, 1024, "bfloat16"), (4096, 4120, 1024, "float16")]
+               (4096, 4100, 1024, "bfloat16"), (4096, 4120, 1024, "float16"), (4096, 4144, 2048, "float16")]
 
 
 @pytest.mark.parametrize("m,n,k,dtype", PEEL_SHAPES)
