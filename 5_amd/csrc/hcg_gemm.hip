@@ -1416,7 +1416,7 @@ __device__ __forceinline__ unsigned char* rs_b() {
 // older load, before LDS reads.  A second block past A's last byte is
 // replaced by the first (its bytes are k >= K, cleared).
 template <int DT, int NB, bool UA = false, int ST = 0>
-__global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
+__global__ __launch_bounds__(NB == 64 ? 512 : 256) void gemm_rowstream_kernel(RowStreamArgs g) {
   static_assert(NB == 16 || NB == 32 || NB == 64, "column block");
   // ST = 3 (NB <= 32, register-staged A): a 72 KB ring, so two workgroups
   // share a CU -- twice the waves to cover the register path's latency
@@ -1424,12 +1424,20 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
   // ahead, 125 against 135 us at 65536 x 8 x 4096).
   constexpr int STAGES = ST ? ST : (NB == 64 ? kRs64Stages : kRsStages);
   static_assert(STAGES >= 3 && STAGES <= 6 && (NB < 64 || STAGES <= kRs64Stages), "stages");
-  constexpr int kChunksB = NB / 8;               // 16-byte chunks per staged B row
-  constexpr int kRowsPerBDma = 64 / kChunksB;    // B rows per DMA instruction
-  constexpr int kBDmaPerWave = kRsStep / kRowsPerBDma / 4;
-  constexpr int kDmaPerWave = 4 + kBDmaPerWave;  // 4 A instructions (16 rows x 256 B)
-  constexpr int kLoadsPerWave = UA ? 8 + kBDmaPerWave : kDmaPerWave;  // memory instructions per stage
-  constexpr int kBlocks = NB / 16;               // MFMA column blocks
+  // NB = 64 runs 8 waves (512 threads): the waves of a pair share a 16-row
+  // block and take 32 columns each, so a CU holds twice the waves at the
+  // same LDS (the register-staged form needs them to cover its latency).
+  constexpr int kWaves = NB == 64 ? 8 : 4;
+  constexpr int kColSplit = kWaves / 4;            // waves per 16-row block
+  constexpr int kRowsPerWave = kRsRows / kWaves;   // A rows each wave loads: 16 or 8
+  constexpr int kAInst = kRowsPerWave / 4;         // A DMA instructions per wave per stage
+  constexpr int kChunksB = NB / 8;                 // 16-byte chunks per staged B row
+  constexpr int kRowsPerBDma = 64 / kChunksB;      // B rows per DMA instruction
+  constexpr int kBDmaPerWave = kRsStep / kRowsPerBDma / kWaves;
+  constexpr int kDmaPerWave = kAInst + kBDmaPerWave;
+  constexpr int kLoadsPerWave = UA ? 2 * kAInst + kBDmaPerWave : kDmaPerWave;  // memory instructions per stage
+  constexpr int kBlocks = NB / 16 / kColSplit;     // MFMA column blocks per wave
+  static_assert(kBDmaPerWave >= 1 && kAInst >= 1, "work split");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1444,14 +1452,15 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
   const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(g.A, g.a_bytes);
   const __amdgpu_buffer_rsrc_t rsrc_b = make_rsrc(g.B, g.b_bytes);
 
-  // DMA roles.  A: wave w loads rows 16w .. 16w+15 in 4 instructions of 4
-  // rows; lane l covers row 4i + l/16 of them at physical chunk l%16, i.e.
-  // logical chunk (l%16) ^ (row%16).  B: wave w loads kBDmaPerWave blocks of
-  // kRowsPerBDma k rows; lane l covers row l / kChunksB, chunk l % kChunksB.
-  int a_off[4], a_col[4];
+  // DMA roles.  A: wave w loads its kRowsPerWave rows from row
+  // kRowsPerWave * w in kAInst instructions of 4 rows; lane l covers row
+  // 4i + l/16 of them at physical chunk l%16, i.e. logical chunk
+  // (l%16) ^ (row%16).  B: wave w loads kBDmaPerWave blocks of kRowsPerBDma
+  // k rows; lane l covers row l / kChunksB, chunk l % kChunksB.
+  int a_off[kAInst], a_col[kAInst];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 16 * wave + 4 * i + (lane >> 4);
+  for (int i = 0; i < kAInst; ++i) {
+    const int row = kRowsPerWave * wave + 4 * i + (lane >> 4);
     const int c = (lane & 15) ^ (row & 15);
     a_col[i] = c * 8;
     a_off[i] = UA ? 0 : ((m0 + row) * g.lda + c * 8) * 2;  // (UA reads through 64-bit pointers)
@@ -1467,17 +1476,17 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
   // UA: register sets of the stages in flight; per A chunk its byte offset
   // in the first block (-1: cleared) and its elements below K.
   using gvec = const __attribute__((address_space(1))) u32x4;
-  u32x4 areg[UA ? STAGES : 1][4][2];
-  int ash[UA ? STAGES : 1][4], avld[UA ? STAGES : 1][4];
+  u32x4 areg[UA ? STAGES : 1][kAInst][2];
+  int ash[UA ? STAGES : 1][kAInst], avld[UA ? STAGES : 1][kAInst];
   u32x4 breg[UA ? STAGES : 1][kBDmaPerWave];
   bool bok[UA ? STAGES : 1][kBDmaPerWave];
   const uintptr_t a_base = reinterpret_cast<uintptr_t>(g.A), b_base = reinterpret_cast<uintptr_t>(g.B);
   const uintptr_t a_end = a_base + ((uintptr_t)(g.M - 1) * g.lda + g.K) * 2;  // one past A's last byte
-  uintptr_t a_rowp[4];
-  bool a_rowok[4];
+  uintptr_t a_rowp[kAInst];
+  bool a_rowok[kAInst];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = m0 + 16 * wave + 4 * i + (lane >> 4);
+  for (int i = 0; i < kAInst; ++i) {
+    const int row = m0 + kRowsPerWave * wave + 4 * i + (lane >> 4);
     a_rowok[i] = row < g.M;
     a_rowp[i] = a_base + (uintptr_t)(a_rowok[i] ? row : 0) * (uintptr_t)g.lda * 2;
   }
@@ -1496,7 +1505,7 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
     const int k0 = step < nsteps ? kbeg + s * kRsStep : kend;
     if constexpr (UA) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kAInst; ++i) {
         const int kc = k0 + a_col[i];  // the chunk's first k
         const bool live = a_rowok[i] && kc < kend;
         const uintptr_t p = live ? a_rowp[i] + (uintptr_t)kc * 2 : a_base;
@@ -1515,8 +1524,8 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        dma16(rsrc_a, (lds_void*)(rs_a<NB, S>() + (16 * wave + 4 * i) * 256),
+      for (int i = 0; i < kAInst; ++i)
+        dma16(rsrc_a, (lds_void*)(rs_a<NB, S>() + (kRowsPerWave * wave + 4 * i) * 256),
               dma_offset(k0 + a_col[i] < kend, a_off[i] + k0 * 2));
 #pragma unroll
       for (int i = 0; i < kBDmaPerWave; ++i)
@@ -1528,7 +1537,8 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
   // Fragment addresses.  A, k step j: row 16w + l%16, chunk 4j + l/16.  B,
   // k step j, column block cb, half h: source lane s = l%16 of group
   // q = l/16 points at k row 32j + 8q + 4h + s/4, column 16cb + 4(s%4).
-  const int a_r = 16 * wave + (lane & 15);
+  const int a_r = 16 * (wave / kColSplit) + (lane & 15);
+  const int col0 = (wave % kColSplit) * (NB / kColSplit);  // this wave's first column
   int fa[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) fa[j] = a_r * 256 + ((4 * j + (lane >> 4)) ^ (a_r & 15)) * 16;
@@ -1540,7 +1550,7 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int sl = lane & 15, q = lane >> 4;
-        fb[j][cb][h] = (32 * j + 8 * q + 4 * h + (sl >> 2)) * (NB * 2) + (16 * cb + 4 * (sl & 3)) * 2;
+        fb[j][cb][h] = (32 * j + 8 * q + 4 * h + (sl >> 2)) * (NB * 2) + (col0 + 16 * cb + 4 * (sl & 3)) * 2;
       }
 
   f32x4 acc[kBlocks];
@@ -1575,13 +1585,13 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
     if constexpr (UA) {
       // This wave's chunks of the stage have landed in registers.
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kAInst; ++i) {
         const int sh = ash[S][i], nv = avld[S][i];
         u32x4 v = sh < 0 ? u32x4{0, 0, 0, 0} : shift_join(areg[S][i][0], areg[S][i][1], sh);
 #pragma unroll
         for (int w = 0; w < 4; ++w)  // elements 2w, 2w + 1 (k >= K cleared)
           v[w] = 2 * w + 1 < nv ? v[w] : (2 * w < nv ? v[w] & 0xffffu : 0u);
-        *reinterpret_cast<u32x4*>(rs_a<NB, S>() + (16 * wave + 4 * i) * 256 + lane * 16) = v;
+        *reinterpret_cast<u32x4*>(rs_a<NB, S>() + (kRowsPerWave * wave + 4 * i) * 256 + lane * 16) = v;
       }
 #pragma unroll
       for (int i = 0; i < kBDmaPerWave; ++i)
@@ -1629,7 +1639,7 @@ __global__ __launch_bounds__(256) void gemm_rowstream_kernel(RowStreamArgs g) {
   for (int cb = 0; cb < kBlocks; ++cb)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = m0 + 16 * wave + (lane >> 4) * 4 + r, col = 16 * cb + (lane & 15);
+      const int row = m0 + 16 * (wave / kColSplit) + (lane >> 4) * 4 + r, col = col0 + 16 * cb + (lane & 15);
       if (row < g.M && col < g.N) dst[(int64_t)row * ld + col] = acc[cb][r];
     }
 }
@@ -2149,10 +2159,11 @@ void launch_rowstream(const RowStreamArgs& a, bool ua, bool short_ring, dim3 gri
       return;
     }
   }
+  const dim3 block(NB == 64 ? 512 : 256);
   if (ua)
-    gemm_rowstream_kernel<DT, NB, true><<<grid, dim3(256), 0, stream>>>(a);
+    gemm_rowstream_kernel<DT, NB, true><<<grid, block, 0, stream>>>(a);
   else
-    gemm_rowstream_kernel<DT, NB, false><<<grid, dim3(256), 0, stream>>>(a);
+    gemm_rowstream_kernel<DT, NB, false><<<grid, block, 0, stream>>>(a);
 }
 
 int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
