@@ -702,6 +702,31 @@ def test_random_shapes_and_layouts_against_oracle(i):
     assert np.all(np.isnan(host[mask]))
 
 
+# Extreme aspect ratios: K in the millions for a 1 x 1 or 3 x 5 output,
+# one-column and one-row outputs of 10^5, K of 1..9, through every kernel
+# that takes the shape, C in a NaN guard band.
+@pytest.mark.parametrize("m,n,k", [(1, 1, 4194304), (3, 5, 1000003), (100000, 1, 10), (1, 100000, 7),
+                                   (70000, 3, 3), (2, 3, 1), (300000, 8, 64), (17, 100000, 9)])
+def test_extreme_shapes(m, n, k):
+    import hc.gfx950 as g
+    from hc.gfx950.workloads import make_inputs
+
+    a, b = make_inputs("c2_4096_f16", seed=m + n + k, m=m, n=n, k=k)
+    want = oracle.gemm_c(a, b)
+    guard = torch.full((m + 2, n + 2), float("nan"), dtype=torch.float32, device=DEV)
+    out = guard[1 : m + 1, 1 : n + 1]
+    for algo in ["auto", "skinny" if m <= 128 else "tiled", "narrow" if n <= 64 else "generic"]:
+        print(f"case extreme {algo} m={m} n={n} k={k}", flush=True)
+        out.fill_(float("nan"))
+        g.gemm(_dev(a), _dev(b), out=out, algo=algo)
+        torch.cuda.synchronize()
+        host = guard.cpu().numpy()
+        _check(host[1 : m + 1, 1 : n + 1], want, k)
+        mask = np.ones_like(host, dtype=bool)
+        mask[1 : m + 1, 1 : n + 1] = False
+        assert np.all(np.isnan(host[mask]))
+
+
 # Operands whose byte offsets reach 2^31 (over 2 GiB): the tiled kernel's
 # WIDE form rebases its buffer resources per tile (A) and per 32-row K
 # step (B).  Inputs are periodic small integers built on the device, so the
