@@ -1351,6 +1351,7 @@ struct RowStreamArgs {
   int kchunk;     // K per split, multiple of kRsStep
   int splits;
   int a_bytes, b_bytes;
+  int rot_groups;  // distinct start steps over the row blocks (>= the run's steps: every step)
 };
 
 #define HCG_RS_STAGE(i)                                                         \
@@ -1495,9 +1496,12 @@ __global__ __launch_bounds__(NB == 64 ? 512 : 256) void gemm_rowstream_kernel(Ro
   // with all blocks starting at the same k, a power-of-two row stride puts
   // every concurrent 256-byte piece at the same address offset modulo the
   // stride, and the reads pile onto a few HBM channels (16384 x 8 x 16384
-  // fp16: 146 us unrotated vs 103 us at K = 16392).  Steps past the run load
-  // zeros.
-  const int rot = (blockIdx.x - split * nrb) % nsteps;
+  // fp16: 146 us unrotated vs 103 us at K = 16392).  With 8 KB rows the
+  // blocks start at 16 evenly spaced steps instead (rot_groups; 65536 x 8 x
+  // 4096: 102 us, against 125 us at every step and 106 us unrotated).  Steps
+  // past the run load zeros.
+  const int rg = min(g.rot_groups, nsteps);
+  const int rot = ((blockIdx.x - split * nrb) % rg) * (nsteps / rg);
   auto issue = [&](auto sc, int step) {
     constexpr int S = decltype(sc)::value;
     int s = step + rot;
@@ -2192,6 +2196,7 @@ int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const 
   if (splits > 16) splits = 16;
   if (splits < 1) splits = 1;
   a.kchunk = (ksteps + splits - 1) / splits * kRsStep;
+  a.rot_groups = lda == 4096 ? 16 : 0x7fffffff;  // measured: 8 KB rows prefer 16 start steps
   a.splits = (K + a.kchunk - 1) / a.kchunk;
   // Workspace: B repacked to zero-padded 16-byte aligned rows (when its rows
   // are not), then the split partials [splits][M][N].
