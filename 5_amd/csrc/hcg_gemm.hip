@@ -2186,15 +2186,17 @@ int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const 
   a.M = M;
   a.N = N;
   a.K = K;
-  // Row blocks, then K splits until the workgroups cover the CUs -- twice
-  // over for register-staged A, whose 3-stage ring fits two workgroups per
-  // CU when N <= 32 (each split at least 4 stages of 128 k).
+  // Row blocks, then the most K splits whose workgroups do not exceed the
+  // CUs -- twice over for register-staged A, whose 3-stage ring fits two
+  // workgroups per CU when N <= 32 (each split at least 4 stages of 128 k).
+  // Rounding up left a short second round: 5000 x 8 x 16384 fp16 39.1 us
+  // at 4 splits (316 workgroups) against 30.3 us at 3.
   const bool a_dma = rowstream_a_dma(A, lda, M, K);
   const bool short_ring = !a_dma && N <= 32;
   const int nrb = (M + kRsRows - 1) / kRsRows;
   const int ksteps = (K + kRsStep - 1) / kRsStep;
   const int target = short_ring ? 2 * st->num_cus : st->num_cus;
-  int splits = (target + nrb - 1) / nrb;
+  int splits = target / nrb;
   const int max_by_k = ksteps / 4 > 0 ? ksteps / 4 : 1;
   if (splits > max_by_k) splits = max_by_k;
   if (splits > 16) splits = 16;
