@@ -967,7 +967,8 @@ constexpr int kStStages = 8;
 constexpr int kStBBytes = kStStep * kStN * 2;  // 8 KB
 constexpr int kStABytes = 16 * kStStep * 2;    // 1 KB per 16-row block of A
 constexpr int kStMaxRowBlocks = 8;              // M <= 128
-constexpr int kStMaxSplits = 16;
+constexpr int kStMaxSplits = 16;      // partials stream_reduce_kernel holds in registers
+constexpr int kStMaxSplitsLoop = 64;  // K splits at all (more than 16: the per-element reduce)
 
 struct StreamArgs {
   const uint16_t* A;
@@ -978,7 +979,7 @@ struct StreamArgs {
   int64_t ldc;
   int M, N, K;
   int kchunk;     // rows per split, multiple of kStStep
-  int splits;     // 1 .. kStMaxSplits
+  int splits;     // 1 .. kStMaxSplitsLoop
   int rblocks;    // 16-row blocks of A: 1, 2, 4 or 8 (M <= 16 * rblocks)
   int a_bytes, b_bytes;
   bool c_vec;     // C rows 16-byte aligned at every 4th column
@@ -1976,21 +1977,23 @@ int skinny_splits(const DeviceState* st, int N, int K) {
 
 // Split count for the streaming kernel: about one workgroup per CU, each
 // split at least 8 stages (256 rows) long.
-// The K split: the most workgroups (column blocks, padded to a multiple of
-// 8, times splits) that do not exceed `per_cu` per CU, each split at least
-// 8 steps.  Overshooting by a few workgroups leaves a short second round:
+// The K split: the most working workgroups (column blocks times splits; the
+// grid's padding workgroups exit at once) that do not exceed `per_cu` per
+// CU, each split at least 8 steps, at most kStMaxSplitsLoop (tiny outputs
+// with a long K: 64 x 32 x 2^20 runs 64 workgroups instead of 16).
+// Overshooting by a few workgroups leaves a short second round:
 // 16 x 12288 x 4096 fp16 28.4 us at 3 splits (288 workgroups) against 22.4
 // us at 2, 16 x 5120 x 13824 40.2 us at 7 against 29.7 at 6.
 int stream_splits(const DeviceState* st, int nblocks, int K, int per_cu) {
   const int ksteps = (K + kStStep - 1) / kStStep;
   int splits = g_skinny_splits_override;
   if (splits <= 0) {
-    splits = per_cu * st->num_cus / (int)round_up(nblocks, 8);
+    splits = per_cu * st->num_cus / nblocks;
     const int max_by_k = ksteps / 8 > 0 ? ksteps / 8 : 1;
     if (splits > max_by_k) splits = max_by_k;
   }
   if (splits > ksteps) splits = ksteps;
-  if (splits > kStMaxSplits) splits = kStMaxSplits;
+  if (splits > kStMaxSplitsLoop) splits = kStMaxSplitsLoop;
   if (splits < 1) splits = 1;
   return splits;
 }
@@ -2010,7 +2013,7 @@ int launch_stream(const StreamArgs& a, hipStream_t stream) {
   }
   HCG_HIP_CHECK(hipGetLastError());
   if (a.splits > 1) {
-    if (a.N % 4 == 0) {
+    if (a.N % 4 == 0 && a.splits <= kStMaxSplits) {
       const int64_t total = (int64_t)a.M * (a.N / 4);
       stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
           a.ws, a.C, a.ldc, a.M, a.N, 16 * a.rblocks, a.splits, a.c_vec);
@@ -2199,7 +2202,7 @@ int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const 
   int splits = target / nrb;
   const int max_by_k = ksteps / 4 > 0 ? ksteps / 4 : 1;
   if (splits > max_by_k) splits = max_by_k;
-  if (splits > 16) splits = 16;
+  if (splits > kStMaxSplitsLoop) splits = kStMaxSplitsLoop;
   if (splits < 1) splits = 1;
   a.kchunk = (ksteps + splits - 1) / splits * kRsStep;
   a.rot_groups = lda == 4096 ? 16 : 0x7fffffff;  // measured: 8 KB rows prefer 16 start steps
@@ -2241,7 +2244,7 @@ int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const 
   }
   HCG_HIP_CHECK(hipGetLastError());
   if (a.splits > 1) {
-    if (N % 4 == 0) {
+    if (N % 4 == 0 && a.splits <= kStMaxSplits) {
       const int64_t total = (int64_t)M * (N / 4);
       stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
           a.ws, C, ldc, M, N, M, a.splits, aligned16(C) && ldc % 4 == 0);
