@@ -968,7 +968,7 @@ constexpr int kStBBytes = kStStep * kStN * 2;  // 8 KB
 constexpr int kStABytes = 16 * kStStep * 2;    // 1 KB per 16-row block of A
 constexpr int kStMaxRowBlocks = 8;              // M <= 128
 constexpr int kStMaxSplits = 16;      // partials stream_reduce_kernel holds in registers
-constexpr int kStMaxSplitsLoop = 64;  // K splits at all (more than 16: the per-element reduce)
+constexpr int kStMaxSplitsLoop = 256;  // K splits at all (more than 16: split_reduce_kernel)
 
 struct StreamArgs {
   const uint16_t* A;
@@ -1687,6 +1687,34 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* ws, flo
   C[(int64_t)row * ldc + col] = v;
 }
 
+// C[i][j] = sum over many splits (more than kStMaxSplits) of ws[s][i][j]
+// (ws rows: `mrows` per split).  A workgroup of kSrWaves waves takes 64
+// consecutive outputs, one per lane (coalesced reads of each split); wave w
+// sums splits w, w + kSrWaves, ... in increasing order and the waves' sums
+// are added in order w = 0 .. kSrWaves - 1: a fixed order, so results repeat
+// bit for bit.  (One element per thread over 256 partials ran at 8x the
+// time: each thread's loads wait on the next.)
+constexpr int kSrWaves = 16;
+__global__ __launch_bounds__(64 * kSrWaves) void split_reduce_kernel(const float* ws, float* C, int64_t ldc,
+                                                                     int M, int N, int mrows, int splits) {
+  __shared__ float sums[kSrWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t idx = (int64_t)blockIdx.x * 64 + lane;
+  const bool live = idx < (int64_t)M * N;
+  const int row = live ? (int)(idx / N) : 0, col = live ? (int)(idx % N) : 0;
+  float v = 0.0f;
+  if (live)
+    for (int sp = wave; sp < splits; sp += kSrWaves) v += ws[((int64_t)sp * mrows + row) * N + col];
+  sums[wave][lane] = v;
+  __syncthreads();
+  if (wave == 0 && live) {
+    float t = sums[0][lane];
+#pragma unroll
+    for (int w = 1; w < kSrWaves; ++w) t += sums[w][lane];
+    C[(int64_t)row * ldc + col] = t;
+  }
+}
+
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* C, int64_t ldc, int M, int N) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)M * N) return;
@@ -1980,7 +2008,7 @@ int skinny_splits(const DeviceState* st, int N, int K) {
 // The K split: the most working workgroups (column blocks times splits; the
 // grid's padding workgroups exit at once) that do not exceed `per_cu` per
 // CU, each split at least 8 steps, at most kStMaxSplitsLoop (tiny outputs
-// with a long K: 64 x 32 x 2^20 runs 64 workgroups instead of 16).
+// with a long K: 64 x 32 x 2^20 runs 256 workgroups instead of 16).
 // Overshooting by a few workgroups leaves a short second round:
 // 16 x 12288 x 4096 fp16 28.4 us at 3 splits (288 workgroups) against 22.4
 // us at 2, 16 x 5120 x 13824 40.2 us at 7 against 29.7 at 6.
@@ -2012,8 +2040,13 @@ int launch_stream(const StreamArgs& a, hipStream_t stream) {
     default: return set_error(HCG_EINVAL, "internal: %d row blocks", a.rblocks);
   }
   HCG_HIP_CHECK(hipGetLastError());
-  if (a.splits > 1) {
-    if (a.N % 4 == 0 && a.splits <= kStMaxSplits) {
+  if (a.splits > kStMaxSplits) {
+    const int64_t total = (int64_t)a.M * a.N;
+    split_reduce_kernel<<<(unsigned)((total + 63) / 64), 64 * kSrWaves, 0, stream>>>(a.ws, a.C, a.ldc, a.M, a.N,
+                                                                                   16 * a.rblocks, a.splits);
+    HCG_HIP_CHECK(hipGetLastError());
+  } else if (a.splits > 1) {
+    if (a.N % 4 == 0) {
       const int64_t total = (int64_t)a.M * (a.N / 4);
       stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
           a.ws, a.C, a.ldc, a.M, a.N, 16 * a.rblocks, a.splits, a.c_vec);
@@ -2243,8 +2276,13 @@ int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const 
     else launch_rowstream<HCG_BF16, 64>(a, !a_dma, short_ring, grid, stream);
   }
   HCG_HIP_CHECK(hipGetLastError());
-  if (a.splits > 1) {
-    if (N % 4 == 0 && a.splits <= kStMaxSplits) {
+  if (a.splits > kStMaxSplits) {
+    const int64_t total = (int64_t)M * N;
+    split_reduce_kernel<<<(unsigned)((total + 63) / 64), 64 * kSrWaves, 0, stream>>>(a.ws, C, ldc, M, N, M,
+                                                                                   a.splits);
+    HCG_HIP_CHECK(hipGetLastError());
+  } else if (a.splits > 1) {
+    if (N % 4 == 0) {
       const int64_t total = (int64_t)M * (N / 4);
       stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
           a.ws, C, ldc, M, N, M, a.splits, aligned16(C) && ldc % 4 == 0);
@@ -2495,15 +2533,16 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
     return HCG_OK;
   }
 
-  // M <= 16, and M <= 128 where the streaming kernel applies, is HBM-bound:
-  // B is streamed once through a skinny kernel instead of occupying only
-  // N/128 workgroups of the tiled kernel.
-  const bool use_skinny = algo == HCG_ALGO_SKINNY ||
-                          (algo == HCG_ALGO_AUTO && (M <= 16 || stream_fits(A, lda, B, ldb, M, N, K)));
-  // N <= 64 (and more than 128 rows) is HBM-bound on A: stream A in 256-byte
-  // row pieces.
-  const bool use_narrow = !use_skinny && (algo == HCG_ALGO_NARROW ||
-                                          (algo == HCG_ALGO_AUTO && rowstream_fits(A, lda, B, ldb, M, N, K)));
+  // N <= 64 is HBM-bound on A: stream A in 256-byte row pieces (for M <=
+  // 128 too -- 64 x 32 x 2^20 fp16: 36 us against 154 us on the skinny
+  // kernel, which streams B in 128-column blocks mostly past N).
+  const bool use_narrow = algo == HCG_ALGO_NARROW ||
+                          (algo == HCG_ALGO_AUTO && rowstream_fits(A, lda, B, ldb, M, N, K));
+  // Otherwise M <= 16, and M <= 128 where the streaming kernel applies, is
+  // HBM-bound: B is streamed once through a skinny kernel instead of
+  // occupying only N/128 workgroups of the tiled kernel.
+  const bool use_skinny = !use_narrow && (algo == HCG_ALGO_SKINNY ||
+                                          (algo == HCG_ALGO_AUTO && (M <= 16 || stream_fits(A, lda, B, ldb, M, N, K))));
   if (algo == HCG_ALGO_NARROW && !rowstream_fits(A, lda, B, ldb, M, N, K))
     return set_error(HCG_EINVAL,
                      "the narrow kernel needs N <= 64 (and offsets of B below 2^31) "

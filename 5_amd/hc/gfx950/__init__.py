@@ -186,10 +186,10 @@ def gemm(a: Any, b: Any, out: Any | None = None, *, algo: str = "auto", device: 
     computed, and copied back into ``out`` (created if None); the call then
     returns after the result is on the host.
 
-    ``algo``: "auto" (the library picks: the streaming kernel for M <= 128,
-    B by DMA when its rows are 16-byte aligned and through registers
-    otherwise; the narrow streaming
-    kernel for N <= 64, A by DMA or through registers likewise;
+    ``algo``: "auto" (the library picks: the narrow streaming kernel for
+    N <= 64, A by DMA when its rows are 16-byte aligned and through
+    registers otherwise; else the streaming kernel for M <= 128, B by DMA
+    or through registers likewise;
     otherwise the LDS-tiled kernel with a modelled tile shape and K split,
     with up to 128 rows or 64 columns past a multiple of 256 peeled off to
     a streaming kernel when that saves a round of tiles),
