@@ -727,6 +727,34 @@ def test_extreme_shapes(m, n, k):
         assert np.all(np.isnan(host[mask]))
 
 
+# Small outputs over a long K: up to 256 K splits, summed past 16 by the
+# split reduce (16 waves per 64 outputs, each a fixed residue class of
+# splits, the waves' sums added in order) -- on the streaming kernel (N > 64)
+# and the narrow one; integer inputs bit-exact and reproducible.
+@pytest.mark.parametrize("m,n,k,algo", [(8, 128, 262144, "skinny"), (100, 200, 131072, "skinny"),
+                                        (64, 32, 262144, "auto"), (200, 8, 262144, "narrow"),
+                                        (16, 130, 65536, "auto")])
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_long_k_many_splits(m, n, k, algo, dtype):
+    from hc.gfx950.workloads import make_inputs
+
+    cfg = "c4_skinny_f16" if dtype == "float16" else "c3_8192_bf16"
+    a, b = make_inputs(cfg, seed=m + n + k, m=m, n=n, k=k)
+    print(f"case long K {algo} {dtype} m={m} n={n} k={k}", flush=True)
+    _check(_gemm(a, b, algo, dtype), oracle.gemm_c(a, b, _dt(dtype)), k)
+
+
+@pytest.mark.parametrize("m,n,k,algo", [(8, 128, 262144, "skinny"), (64, 32, 262144, "narrow")])
+def test_long_k_many_splits_integer_bit_exact_and_reproducible(m, n, k, algo):
+    rng = np.random.default_rng(m * n)
+    ai = rng.integers(-2, 3, size=(m, k))
+    bi = rng.integers(-2, 3, size=(k, n))
+    want = (ai.astype(np.float64) @ bi.astype(np.float64)).astype(np.float32)  # |sums| <= 2^20
+    first = _gemm(ai.astype(np.float16), bi.astype(np.float16), algo)
+    assert np.array_equal(first, want)
+    assert np.array_equal(first.view(np.uint32), _gemm(ai.astype(np.float16), bi.astype(np.float16), algo).view(np.uint32))
+
+
 # Operands whose byte offsets reach 2^31 (over 2 GiB): the tiled kernel's
 # WIDE form rebases its buffer resources per tile (A) and per 32-row K
 # step (B).  Inputs are periodic small integers built on the device, so the
