@@ -1744,9 +1744,14 @@ constexpr int kMaxStreamWorkspaces = 16;
 // Library-owned scratch (split-K partials, repacked operands), one grow-only
 // buffer per (device, stream) so that concurrent streams never share it.  A
 // buffer handed out while its stream is being captured into a HIP graph is
-// pinned: the graph keeps its address, so it is never freed or reused for
-// another stream afterwards; when its slot needs a larger or a different
-// buffer, the pinned one is retired (kept allocated until the process ends).
+// pinned: the graph keeps its address, so it is never freed, and no eager
+// call uses it again -- the first call on its stream that is not being
+// captured retires it (kept allocated until the process ends) and takes a
+// fresh buffer, so a replay never races with eager work.  Graphs captured
+// on one stream with no eager call on that stream between the captures
+// share one pinned buffer.  With more than kMaxStreamWorkspaces streams in
+// use, slots are evicted round-robin; an evicted buffer is freed with
+// hipFree, which synchronises the device.
 struct Workspace {
   void* stream = nullptr;
   void* ptr = nullptr;
@@ -1820,7 +1825,7 @@ int stream_workspace(DeviceState* st, hipStream_t stream, size_t bytes, void** o
     w = &st->ws[st->ws_next];
     st->ws_next = (st->ws_next + 1) % kMaxStreamWorkspaces;
   }
-  if (w->ptr && (w->stream != (void*)stream || w->bytes < bytes)) {
+  if (w->ptr && (w->stream != (void*)stream || w->bytes < bytes || (w->pinned && !capturing))) {
     if (w->pinned) {
       st->retired.push_back(w->ptr);
     } else {
@@ -1845,6 +1850,68 @@ int stream_workspace(DeviceState* st, hipStream_t stream, size_t bytes, void** o
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Where a call's scratch comes from: its stream's library workspace
+// (allocated on demand, see stream_workspace), or a fixed device buffer of
+// `cap` bytes that is never grown (hcg_gemm_noalloc).  Planners that size
+// split-K partials keep them within room(); repacked operands must fit.
+struct Scratch {
+  DeviceState* st = nullptr;
+  hipStream_t stream = nullptr;
+  void* fixed = nullptr;
+  size_t cap = 0;
+
+  // Bytes available for split partials once `used` bytes are taken.
+  size_t room(size_t used) const {
+    if (!fixed) return SIZE_MAX;
+    return used < cap ? cap - used : 0;
+  }
+};
+
+int get_scratch(const Scratch& sc, size_t bytes, void** out) {
+  if (sc.fixed) {
+    if (bytes > sc.cap)
+      return set_error(HCG_EINVAL,
+                       "this call needs %zu bytes of scratch (repacked operands and split partials); the "
+                       "allocation-free entry point has %zu",
+                       bytes, sc.cap);
+    *out = sc.fixed;
+    return HCG_OK;
+  }
+  return stream_workspace(sc.st, sc.stream, bytes, out);
+}
+
+// Largest split count (at most `splits`, at least 1) whose partials of
+// `per_split` bytes each fit in `room` bytes.
+int fit_splits(int splits, size_t per_split, size_t room) {
+  if (per_split == 0 || room == SIZE_MAX) return splits;
+  const size_t most = room / per_split;
+  if ((size_t)splits > most) splits = most >= 2 ? (int)most : 1;
+  return splits;
+}
+
+// Sums `splits` partial slices ws[s][0 .. mrows)[0 .. N) into the M x N
+// output C in the fixed order s = 0 .. splits - 1 (bit-reproducible): past
+// kStMaxSplits with a wave per residue class of splits, else four columns
+// per thread when N is a multiple of 4 (16-byte partial rows: the
+// workspace base is 256-byte aligned), else one element per thread.
+int launch_reduce(const float* ws, float* C, int64_t ldc, int M, int N, int mrows, int splits, bool c_vec,
+                  hipStream_t stream) {
+  if (splits > kStMaxSplits) {
+    const int64_t total = (int64_t)M * N;
+    split_reduce_kernel<<<(unsigned)((total + 63) / 64), 64 * kSrWaves, 0, stream>>>(ws, C, ldc, M, N, mrows,
+                                                                                   splits);
+  } else if (N % 4 == 0) {
+    const int64_t total = (int64_t)M * (N / 4);
+    stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(ws, C, ldc, M, N, mrows, splits,
+                                                                             c_vec);
+  } else {
+    const int64_t total = (int64_t)M * N;
+    skinny_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(ws, C, ldc, M, N, mrows, splits);
+  }
+  HCG_HIP_CHECK(hipGetLastError());
+  return HCG_OK;
+}
 
 template <int DT>
 int launch_generic(const TiledArgs& a, bool vec_a, bool vec_b, hipStream_t stream) {
@@ -1901,10 +1968,13 @@ constexpr int kSplitCandidates[] = {1, 2, 3, 4, 6, 8};
 constexpr int kMinKTilesPerSplit = 8;
 constexpr size_t kMaxSplitWorkspace = (size_t)512 << 20;
 
-bool split_ok(int splits, int M, int N, int K) {
+// `room`: scratch bytes available for the partials (kMaxSplitWorkspace at
+// most).
+bool split_ok(int splits, int M, int N, int K, size_t room) {
   const int nk = (K + kDmaK - 1) / kDmaK;
+  const size_t limit = room < kMaxSplitWorkspace ? room : kMaxSplitWorkspace;
   return splits == 1 || (splits <= 64 && (nk + splits - 1) / splits >= kMinKTilesPerSplit &&
-                         (size_t)splits * M * N * sizeof(float) <= kMaxSplitWorkspace);
+                         (size_t)splits * M * N * sizeof(float) <= limit);
 }
 
 double plan_cost(const TileShape& t, int splits, int num_cus, int M, int N, int K) {
@@ -1923,11 +1993,11 @@ double plan_cost(const TileShape& t, int splits, int num_cus, int M, int N, int 
 }
 
 TilePlan plan_tiles(int num_cus, int M, int N, int K, int force_shape, bool allow_split,
-                    double* cost_out = nullptr) {
+                    double* cost_out = nullptr, size_t room = kMaxSplitWorkspace) {
   TilePlan best{force_shape >= 0 ? force_shape : 0, 1};
   double best_cost = -1;
   const int forced_splits =
-      allow_split && g_tiled_splits_override > 0 && split_ok(g_tiled_splits_override, M, N, K)
+      allow_split && g_tiled_splits_override > 0 && split_ok(g_tiled_splits_override, M, N, K, room)
           ? g_tiled_splits_override
           : 0;
   for (int i = 0; i < kNumTileShapes; ++i) {
@@ -1937,7 +2007,7 @@ TilePlan plan_tiles(int num_cus, int M, int N, int K, int force_shape, bool allo
     for (int c = 0; c < (forced_splits > 0 ? 1 : (int)(sizeof(kSplitCandidates) / sizeof(int))); ++c) {
       const int splits = forced_splits > 0 ? forced_splits : kSplitCandidates[c];
       if (splits > 1 && !allow_split) break;
-      if (!split_ok(splits, M, N, K)) continue;
+      if (!split_ok(splits, M, N, K, room)) continue;
       const double cost = plan_cost(t, splits, num_cus, M, N, K);
       if (best_cost < 0 || cost < best_cost) {
         best = TilePlan{i, splits};
@@ -2042,23 +2112,7 @@ int launch_stream(const StreamArgs& a, hipStream_t stream) {
     default: return set_error(HCG_EINVAL, "internal: %d row blocks", a.rblocks);
   }
   HCG_HIP_CHECK(hipGetLastError());
-  if (a.splits > kStMaxSplits) {
-    const int64_t total = (int64_t)a.M * a.N;
-    split_reduce_kernel<<<(unsigned)((total + 63) / 64), 64 * kSrWaves, 0, stream>>>(a.ws, a.C, a.ldc, a.M, a.N,
-                                                                                   16 * a.rblocks, a.splits);
-    HCG_HIP_CHECK(hipGetLastError());
-  } else if (a.splits > 1) {
-    if (a.N % 4 == 0) {
-      const int64_t total = (int64_t)a.M * (a.N / 4);
-      stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
-          a.ws, a.C, a.ldc, a.M, a.N, 16 * a.rblocks, a.splits, a.c_vec);
-    } else {
-      const int64_t total = (int64_t)a.M * a.N;
-      skinny_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(a.ws, a.C, a.ldc, a.M, a.N,
-                                                                               16 * a.rblocks, a.splits);
-    }
-    HCG_HIP_CHECK(hipGetLastError());
-  }
+  if (a.splits > 1) return launch_reduce(a.ws, a.C, a.ldc, a.M, a.N, 16 * a.rblocks, a.splits, a.c_vec, stream);
   return HCG_OK;
 }
 
@@ -2092,8 +2146,10 @@ bool stream_fits(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t
          (stream_a_in_place(A, lda, M, K) || stream_extent_a(round_up(K, 8), M, K));
 }
 
-int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
-               float* C, int64_t ldc, int M, int N, int K, hipStream_t stream) {
+int run_skinny(const Scratch& sc, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
+               float* C, int64_t ldc, int M, int N, int K) {
+  DeviceState* st = sc.st;
+  hipStream_t stream = sc.stream;
   if (stream_fits(A, lda, B, ldb, M, N, K)) {
     const bool a_in_place = stream_a_in_place(A, lda, M, K);
     const int64_t lda_use = a_in_place ? lda : (int64_t)round_up(K, 8);
@@ -2111,7 +2167,9 @@ int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const voi
     // for one or two row blocks (16 x 8191 x 8192 fp16: 39.9 -> 37.3 us; at
     // four row blocks the larger partials cost more than that gains).
     const bool b_dma = stream_b_dma(B, ldb, N, K);
+    const size_t a_sz = a_in_place ? 0 : round_up((size_t)M * lda_use * 2, 256);
     a.splits = stream_splits(st, (N + kStN - 1) / kStN, K, !b_dma && stream_rblocks(M) <= 2 ? 2 : 1);
+    a.splits = fit_splits(a.splits, (size_t)16 * stream_rblocks(M) * N * sizeof(float), sc.room(a_sz));
     const int ksteps = (K + kStStep - 1) / kStStep;
     a.kchunk = ((ksteps + a.splits - 1) / a.splits) * kStStep;
     a.splits = (K + a.kchunk - 1) / a.kchunk;  // drop empty trailing splits
@@ -2123,11 +2181,10 @@ int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const voi
     a.ws = nullptr;
     // Workspace: A repacked (when it cannot be used in place), then the
     // split partials.
-    const size_t a_sz = a_in_place ? 0 : round_up((size_t)M * lda_use * 2, 256);
     const size_t p_sz = a.splits > 1 ? (size_t)a.splits * 16 * a.rblocks * (size_t)N * sizeof(float) : 0;
     if (a_sz + p_sz > 0) {
       void* ws = nullptr;
-      const int rc = stream_workspace(st, stream, a_sz + p_sz, &ws);
+      const int rc = get_scratch(sc, a_sz + p_sz, &ws);
       if (rc != HCG_OK) return rc;
       if (!a_in_place) {
         uint16_t* a_p = static_cast<uint16_t*>(ws);
@@ -2161,7 +2218,7 @@ int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const voi
   a.M = M;
   a.N = N;
   a.K = K;
-  a.splits = skinny_splits(st, N, K);
+  a.splits = fit_splits(skinny_splits(st, N, K), (size_t)16 * N * sizeof(float), sc.room(0));
   const int kunit = kSkinnyStep * kSkinnyWaves;
   const int kunits = (K + kunit - 1) / kunit;
   a.kchunk = ((kunits + a.splits - 1) / a.splits) * kunit;
@@ -2169,7 +2226,7 @@ int run_skinny(DeviceState* st, int dtype, const void* A, int64_t lda, const voi
   a.ws = nullptr;
   if (a.splits > 1) {
     void* ws = nullptr;
-    const int rc = stream_workspace(st, stream, (size_t)a.splits * 16 * (size_t)N * sizeof(float), &ws);
+    const int rc = get_scratch(sc, (size_t)a.splits * 16 * (size_t)N * sizeof(float), &ws);
     if (rc != HCG_OK) return rc;
     a.ws = static_cast<float*>(ws);
   }
@@ -2212,8 +2269,10 @@ void launch_rowstream(const RowStreamArgs& a, bool ua, bool short_ring, dim3 gri
     gemm_rowstream_kernel<DT, NB, false><<<grid, block, 0, stream>>>(a);
 }
 
-int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
-                  float* C, int64_t ldc, int M, int N, int K, hipStream_t stream) {
+int run_rowstream(const Scratch& sc, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
+                  float* C, int64_t ldc, int M, int N, int K) {
+  DeviceState* st = sc.st;
+  hipStream_t stream = sc.stream;
   RowStreamArgs a{};
   a.A = static_cast<const uint16_t*>(A);
   a.B = static_cast<const uint16_t*>(B);
@@ -2239,18 +2298,19 @@ int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const 
   if (splits > max_by_k) splits = max_by_k;
   if (splits > kStMaxSplitsLoop) splits = kStMaxSplitsLoop;
   if (splits < 1) splits = 1;
-  a.kchunk = (ksteps + splits - 1) / splits * kRsStep;
-  a.rot_groups = lda == 4096 ? 16 : 0x7fffffff;  // measured: 8 KB rows prefer 16 start steps
-  a.splits = (K + a.kchunk - 1) / a.kchunk;
   // Workspace: B repacked to zero-padded 16-byte aligned rows (when its rows
   // are not), then the split partials [splits][M][N].
   const bool b_ok = aligned16(B) && ldb % 8 == 0;
   const int64_t ldb_use = b_ok ? ldb : round_up(N, 8);
   const size_t b_sz = b_ok ? 0 : round_up((size_t)K * ldb_use * 2, 256);
+  splits = fit_splits(splits, (size_t)M * N * sizeof(float), sc.room(b_sz));
+  a.kchunk = (ksteps + splits - 1) / splits * kRsStep;
+  a.rot_groups = lda == 4096 ? 16 : 0x7fffffff;  // measured: 8 KB rows prefer 16 start steps
+  a.splits = (K + a.kchunk - 1) / a.kchunk;
   const size_t p_sz = a.splits > 1 ? (size_t)a.splits * M * N * sizeof(float) : 0;
   if (b_sz + p_sz > 0) {
     void* ws = nullptr;
-    const int rc = stream_workspace(st, stream, b_sz + p_sz, &ws);
+    const int rc = get_scratch(sc, b_sz + p_sz, &ws);
     if (rc != HCG_OK) return rc;
     if (!b_ok) {
       uint16_t* b_p = static_cast<uint16_t*>(ws);
@@ -2278,22 +2338,7 @@ int run_rowstream(DeviceState* st, int dtype, const void* A, int64_t lda, const 
     else launch_rowstream<HCG_BF16, 64>(a, !a_dma, short_ring, grid, stream);
   }
   HCG_HIP_CHECK(hipGetLastError());
-  if (a.splits > kStMaxSplits) {
-    const int64_t total = (int64_t)M * N;
-    split_reduce_kernel<<<(unsigned)((total + 63) / 64), 64 * kSrWaves, 0, stream>>>(a.ws, C, ldc, M, N, M,
-                                                                                   a.splits);
-    HCG_HIP_CHECK(hipGetLastError());
-  } else if (a.splits > 1) {
-    if (N % 4 == 0) {
-      const int64_t total = (int64_t)M * (N / 4);
-      stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
-          a.ws, C, ldc, M, N, M, a.splits, aligned16(C) && ldc % 4 == 0);
-    } else {
-      const int64_t total = (int64_t)M * N;
-      skinny_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(a.ws, C, ldc, M, N, M, a.splits);
-    }
-    HCG_HIP_CHECK(hipGetLastError());
-  }
+  if (a.splits > 1) return launch_reduce(a.ws, C, ldc, M, N, M, a.splits, aligned16(C) && ldc % 4 == 0, stream);
   return HCG_OK;
 }
 
@@ -2327,9 +2372,10 @@ int64_t fast_extent_b(int N, int K, int64_t ldb) {
   return ((int64_t)round_up(K, kTileK) * ldb + round_up(N, kTileN) + 8) * 2;
 }
 
-int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
-              float* C, int64_t ldc, int M, int N, int K, hipStream_t stream, bool force_generic,
-              int force_shape) {
+int run_tiled(const Scratch& sc, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
+              float* C, int64_t ldc, int M, int N, int K, bool force_generic, int force_shape) {
+  DeviceState* st = sc.st;
+  hipStream_t stream = sc.stream;
   const int64_t kLimit = (int64_t)1 << 31;
   // The DMA kernel masks at 8-element granularity.  A also needs K a
   // multiple of 8 (or zero padding supplied by a repack): a chunk straddling
@@ -2369,20 +2415,20 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
     return dtype == HCG_F16 ? launch_dma<HCG_F16, true>(f, plan.shape, stream)
                             : launch_dma<HCG_BF16, true>(f, plan.shape, stream);
   }
-  // Explicit tile shapes run without a K split; "auto" and "tiled" may split.
-  const TilePlan plan = plan_tiles(st->num_cus, M, N, K, force_shape, force_shape < 0);
-  const TileShape& ts = kTileShapes[plan.shape];
-  if ((int64_t)((M + ts.tm - 1) / ts.tm) * ((N + ts.tn - 1) / ts.tn) * plan.splits > 0x7fffffff)
-    return run_generic(dtype, A, lda, B, ldb, C, ldc, M, N, K, stream);
-
   // Workspace: repacked operands (rows not 16-byte aligned), then the split
   // partials [splits][M][N].
   const size_t a_sz = a_ok ? 0 : round_up((size_t)M * lda_p * 2, 256);
   const size_t b_sz = b_ok ? 0 : round_up((size_t)K * ldb_p * 2, 256);
+  // Explicit tile shapes run without a K split; "auto" and "tiled" may split.
+  const TilePlan plan = plan_tiles(st->num_cus, M, N, K, force_shape, force_shape < 0, nullptr,
+                                   sc.room(a_sz + b_sz));
+  const TileShape& ts = kTileShapes[plan.shape];
+  if ((int64_t)((M + ts.tm - 1) / ts.tm) * ((N + ts.tn - 1) / ts.tn) * plan.splits > 0x7fffffff)
+    return run_generic(dtype, A, lda, B, ldb, C, ldc, M, N, K, stream);
   const size_t p_sz = plan.splits > 1 ? (size_t)plan.splits * M * N * sizeof(float) : 0;
   void* ws = nullptr;
   if (a_sz + b_sz + p_sz > 0) {
-    const int rc = stream_workspace(st, stream, a_sz + b_sz + p_sz, &ws);
+    const int rc = get_scratch(sc, a_sz + b_sz + p_sz, &ws);
     if (rc != HCG_OK) return rc;
   }
   const uint16_t* a_use = static_cast<const uint16_t*>(A);
@@ -2434,16 +2480,7 @@ int run_tiled(DeviceState* st, int dtype, const void* A, int64_t lda, const void
   const int rc = dtype == HCG_F16 ? launch_dma<HCG_F16, false>(f, plan.shape, stream)
                                   : launch_dma<HCG_BF16, false>(f, plan.shape, stream);
   if (rc != HCG_OK || f.splits == 1) return rc;
-  if (N % 4 == 0) {
-    const int64_t total = (int64_t)M * (N / 4);
-    stream_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(f.ws, C, ldc, M, N, M, f.splits,
-                                                                             aligned16(C) && ldc % 4 == 0);
-  } else {
-    const int64_t total = (int64_t)M * N;
-    skinny_reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(f.ws, C, ldc, M, N, M, f.splits);
-  }
-  HCG_HIP_CHECK(hipGetLastError());
-  return HCG_OK;
+  return launch_reduce(f.ws, C, ldc, M, N, M, f.splits, aligned16(C) && ldc % 4 == 0, stream);
 }
 
 // Remainder peeling (HCG_ALGO_AUTO only).  A few rows or columns past a
@@ -2496,8 +2533,11 @@ Peel plan_peel(const DeviceState* st, const void* A, int64_t lda, const void* B,
   return p;
 }
 
+// `fixed` / `fixed_bytes`: a caller-owned scratch buffer that replaces the
+// stream's library workspace (nothing is allocated); null for the default.
 int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
-              float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream_ptr) {
+              float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream_ptr,
+              void* fixed = nullptr, size_t fixed_bytes = 0) {
   if (dtype != HCG_F16 && dtype != HCG_BF16)
     return set_error(HCG_EINVAL, "dtype must be HCG_F16 (0) or HCG_BF16 (1), got %d", dtype);
   if (algo < HCG_ALGO_AUTO || algo > HCG_ALGO_NARROW)
@@ -2549,31 +2589,37 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
     return set_error(HCG_EINVAL,
                      "the narrow kernel needs N <= 64 (and offsets of B below 2^31) "
                      "(M=%lld N=%lld K=%lld)", (long long)M, (long long)N, (long long)K);
+  Scratch sc;
+  sc.st = st;
+  sc.stream = stream;
+  sc.fixed = fixed;
+  sc.cap = fixed_bytes;
   // Workspaces stay valid while ws_mutex is held (see stream_workspace), so
-  // the lock covers the launches too; a launch only enqueues work.
+  // the lock covers the launches too; a launch only enqueues work.  The two
+  // launches of a peeled shape share the scratch in stream order.
   std::lock_guard<std::mutex> lock(st->ws_mutex);
   if (use_narrow) {
-    rc = run_rowstream(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream);
+    rc = run_rowstream(sc, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K);
   } else if (use_skinny) {
-    rc = run_skinny(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream);
+    rc = run_skinny(sc, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K);
   } else {
     const int force_shape = algo >= HCG_ALGO_TILED_256x256 ? algo - HCG_ALGO_TILED_256x256 : -1;
     const Peel peel = algo == HCG_ALGO_AUTO ? plan_peel(st, A, lda, B, ldb, (int)M, (int)N, (int)K) : Peel{};
     if (peel.rows > 0) {
       const int mm = (int)M - peel.rows;
-      rc = run_tiled(st, dtype, A, lda, B, ldb, C, ldc, mm, (int)N, (int)K, stream, false, -1);
+      rc = run_tiled(sc, dtype, A, lda, B, ldb, C, ldc, mm, (int)N, (int)K, false, -1);
       if (rc == HCG_OK)
-        rc = run_skinny(st, dtype, static_cast<const uint16_t*>(A) + (int64_t)mm * lda, lda, B, ldb,
-                        C + (int64_t)mm * ldc, ldc, peel.rows, (int)N, (int)K, stream);
+        rc = run_skinny(sc, dtype, static_cast<const uint16_t*>(A) + (int64_t)mm * lda, lda, B, ldb,
+                        C + (int64_t)mm * ldc, ldc, peel.rows, (int)N, (int)K);
     } else if (peel.cols > 0) {
       const int nn = (int)N - peel.cols;
-      rc = run_tiled(st, dtype, A, lda, B, ldb, C, ldc, (int)M, nn, (int)K, stream, false, -1);
+      rc = run_tiled(sc, dtype, A, lda, B, ldb, C, ldc, (int)M, nn, (int)K, false, -1);
       if (rc == HCG_OK)
-        rc = run_rowstream(st, dtype, A, lda, static_cast<const uint16_t*>(B) + nn, ldb, C + nn, ldc, (int)M,
-                           peel.cols, (int)K, stream);
+        rc = run_rowstream(sc, dtype, A, lda, static_cast<const uint16_t*>(B) + nn, ldb, C + nn, ldc, (int)M,
+                           peel.cols, (int)K);
     } else {
-      rc = run_tiled(st, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, stream,
-                     algo == HCG_ALGO_GENERIC, force_shape);
+      rc = run_tiled(sc, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, algo == HCG_ALGO_GENERIC,
+                     force_shape);
     }
   }
   if (rc == HCG_OK) t_last_error.clear();

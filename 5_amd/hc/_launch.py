@@ -189,6 +189,54 @@ def default_group_shape(work_shape: tuple[int, ...], subgroup_size: int | None) 
     return (_align_up(base[0], subgroup_size), *base[1:])
 
 
+@dataclass(frozen=True)
+class LaunchGeometry:
+    env: Env
+    literal_names: frozenset[str]
+    work_shape: tuple[int, ...]
+    group_shape: tuple[int, ...]
+    subgroup_size: int | None
+
+
+def _geometry(metadata: KernelMetadata, env: Env, target: Any) -> LaunchGeometry:
+    literal_names = frozenset(s.name for s in metadata.literals if isinstance(s, Symbol))
+    work_shape = _resolve_shape(metadata.work_shape, env, literal_names)
+    subgroup_size = (
+        None
+        if metadata.subgroup_size is None
+        else _resolve_dim(metadata.subgroup_size, env, literal_names, static=True, name="subgroup_size")
+    )
+    if metadata.group_shape is None:
+        chooser = getattr(target, "choose_group_shape", None)
+        group_shape = (
+            chooser(work_shape, subgroup_size)
+            if chooser is not None
+            else default_group_shape(work_shape, subgroup_size)
+        )
+    else:
+        group_shape = _resolve_shape(metadata.group_shape, env, literal_names)
+    _validate(work_shape, group_shape, subgroup_size, getattr(target, "max_group_size", None))
+    return LaunchGeometry(env, literal_names, work_shape, group_shape, subgroup_size)
+
+
+def launch_geometry(fn: Any, shapes: dict[str, tuple[int, ...]], target: Any = None) -> LaunchGeometry:
+    """Geometry of a launch whose Buffer parameters have the given shapes
+    (no argument values: used to plan a launch before buffers exist)."""
+    try:
+        metadata = kernel_metadata(fn)
+        annotations = resolved_annotations(fn)
+        bindings = Bindings()
+        for name, shape in shapes.items():
+            spec = annotations.get(name)
+            if not isinstance(spec, BufferSpec) or len(spec.dimensions) != len(shape):
+                raise LaunchError(f"{name} is not a Buffer of rank {len(shape)}")
+            for index, dim in enumerate(spec.dimensions):
+                _bind_dimension(bindings, dim, int(shape[index]), f"{name}.shape[{index}]")
+        return _geometry(metadata, bindings.freeze(), target)
+    except SymbolError as exc:
+        raise LaunchError(str(exc)) from exc
+
+
 def prepare_launch(fn: Any, args: tuple[Any, ...], kwargs: dict[str, Any], target: Any) -> PreparedLaunch:
     try:
         metadata = kernel_metadata(fn)
@@ -203,33 +251,16 @@ def prepare_launch(fn: Any, args: tuple[Any, ...], kwargs: dict[str, Any], targe
                 buffer_params.append(name)
             elif get_origin(annotation) is tuple:
                 _bind_tuple(bindings, get_args(annotation), value, name)
-        env = bindings.freeze()
-        literal_names = frozenset(s.name for s in metadata.literals if isinstance(s, Symbol))
-        work_shape = _resolve_shape(metadata.work_shape, env, literal_names)
-        subgroup_size = (
-            None
-            if metadata.subgroup_size is None
-            else _resolve_dim(metadata.subgroup_size, env, literal_names, static=True, name="subgroup_size")
-        )
-        if metadata.group_shape is None:
-            chooser = getattr(target, "choose_group_shape", None)
-            group_shape = (
-                chooser(work_shape, subgroup_size)
-                if chooser is not None
-                else default_group_shape(work_shape, subgroup_size)
-            )
-        else:
-            group_shape = _resolve_shape(metadata.group_shape, env, literal_names)
-        _validate(work_shape, group_shape, subgroup_size, getattr(target, "max_group_size", None))
+        geometry = _geometry(metadata, bindings.freeze(), target)
     except SymbolError as exc:
         raise LaunchError(str(exc)) from exc
     return PreparedLaunch(
         fn=fn,
         bound=bound,
-        env=env,
-        literal_names=literal_names,
-        work_shape=work_shape,
-        group_shape=group_shape,
-        subgroup_size=subgroup_size,
+        env=geometry.env,
+        literal_names=geometry.literal_names,
+        work_shape=geometry.work_shape,
+        group_shape=geometry.group_shape,
+        subgroup_size=geometry.subgroup_size,
         buffer_params=tuple(buffer_params),
     )

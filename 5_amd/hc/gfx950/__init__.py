@@ -10,20 +10,24 @@ interpreting it workgroup by workgroup.
 Kernels are lowered as a whole, not intrinsic by intrinsic: the wave64 MFMA
 design replaces the reference's per-lane wave32 WMMA fragment contract
 (examples/amdgpu_gfx11_wmma_matmul.py:18-31), so no per-intrinsic mapping
-exists.  A kernel is accepted when
+exists.  A kernel runs on gfx950 when
 
-* it was registered with :func:`register_kernel`, or
-* its name is one of :data:`KNOWN_GEMM_KERNELS` (the reference's
-  ``tiled_gfx11_wmma_matmul``, examples/amdgpu_gfx11_wmma_matmul.py:301-326,
-  and this package's ``tiled_gfx950_mfma_matmul``) and its buffer
-  signature is the contraction ``(Buffer[M, K, T], Buffer[K, N, T],
-  Buffer[M, N, float32])`` with T float16 or bfloat16.
+* its body is the tiled contraction of
+  examples/amdgpu_gfx11_wmma_matmul.py:306-326 (any tile extents), checked
+  statement by statement and by a recorded CPU run of a small ragged launch
+  through the kernel's own helpers and intrinsic fallbacks, whose intrinsic
+  carries a lowering for an amdgpu target (see ``_contract``) -- the
+  reference's ``tiled_gfx11_wmma_matmul`` and this package's
+  ``tiled_gfx950_mfma_matmul`` both are; or
+* a lowering callable was registered for it with :func:`register_kernel`.
 
-Anything else raises ``LaunchError`` naming the kernel.
+Anything else raises ``LaunchError`` naming the kernel and the reason; the
+kernel's name plays no part.
 """
 
 from __future__ import annotations
 
+import functools
 import os
 from collections.abc import Callable
 from dataclasses import dataclass
@@ -32,14 +36,9 @@ from typing import Any
 import numpy as np
 
 from .._errors import BackendError, LaunchError
-from .._launch import PreparedLaunch, buffer_dtype_name, prepare_launch, resolved_annotations
-from ..core import BufferSpec
-from ..symbols import Symbol
+from .._launch import PreparedLaunch, buffer_dtype_name, prepare_launch
 from . import _native
-
-TARGET_NAME = "amdgpu-gfx950"
-
-KNOWN_GEMM_KERNELS = frozenset({"tiled_gfx11_wmma_matmul", "tiled_gfx950_mfma_matmul"})
+from ._contract import TARGET_NAME, Contraction, gemm_signature, recognise
 
 _DTYPE_CODES = {"float16": _native.HCG_F16, "bfloat16": _native.HCG_BF16}
 _TORCH_DTYPE_CODES: dict[Any, int] = {}
@@ -70,6 +69,26 @@ class Gfx950Target:
         return (-(-base[0] // subgroup_size) * subgroup_size, *base[1:])
 
 
+@functools.lru_cache(maxsize=1)
+def device_available() -> bool:
+    """True when the library is built and a gfx950 GPU is visible: then a
+    launch with ``target=None`` runs here."""
+    if not os.path.exists(_native.LIB_PATH):
+        return False
+    try:
+        import torch
+    except ImportError:
+        return False
+    if not torch.cuda.is_available():
+        return False
+    try:
+        index = torch.cuda.current_device()
+        arch = getattr(torch.cuda.get_device_properties(index), "gcnArchName", "") or ""
+    except (RuntimeError, AssertionError):
+        return False
+    return arch.split(":")[0] == "gfx950"
+
+
 # --------------------------------------------------------------------------
 # Kernel lowering registry
 # --------------------------------------------------------------------------
@@ -79,45 +98,28 @@ Lowering = Callable[[PreparedLaunch, Gfx950Target], None]
 _LOWERINGS: dict[Any, Lowering] = {}
 
 
-def _gemm_signature(fn: Any) -> tuple[str, str, str] | None:
-    """Names of the (A, B, C) parameters if ``fn`` has the contraction
-    signature, else None."""
-    annotations = resolved_annotations(fn)
-    specs = [(name, spec) for name, spec in annotations.items() if isinstance(spec, BufferSpec)]
-    if len(specs) != 3:
-        return None
-    (na, a), (nb, b), (nc, c) = specs
-    if not all(len(s.dimensions) == 2 for s in (a, b, c)):
-        return None
-    if not all(isinstance(d, Symbol) for s in (a, b, c) for d in s.dimensions):
-        return None
-    m, k = a.dimensions
-    k2, n = b.dimensions
-    m2, n2 = c.dimensions
-    if not (k == k2 and m == m2 and n == n2) or len({m, n, k}) != 3:
-        return None
-    if a.dtype != b.dtype or a.dtype not in _DTYPE_CODES or c.dtype != "float32":
-        return None
-    return na, nb, nc
+def _contraction_lowering(contraction: Contraction) -> Lowering:
+    def lower(prepared: PreparedLaunch, target: Gfx950Target) -> None:
+        args = prepared.bound.arguments
+        gemm(args[contraction.a], args[contraction.b], out=args[contraction.c], algo=target.algo,
+             device=target.device)
 
-
-def _gemm_lowering(prepared: PreparedLaunch, target: Gfx950Target) -> None:
-    names = _gemm_signature(prepared.fn)
-    if names is None:
-        raise LaunchError(f"{prepared.fn.__name__} does not have a GEMM buffer signature")
-    args = prepared.bound.arguments
-    gemm(args[names[0]], args[names[1]], out=args[names[2]], algo=target.algo, device=target.device)
+    lower.contraction = contraction  # type: ignore[attr-defined]
+    return lower
 
 
 def register_kernel(fn: Any, lowering: Lowering | str = "gemm") -> Any:
-    """Register a gfx950 lowering for kernel ``fn``.  ``"gemm"`` selects the
-    built-in GEMM lowering (the kernel must have the contraction signature)."""
+    """Register a gfx950 lowering for kernel ``fn``.
+
+    ``"gemm"`` checks now that ``fn`` is the tiled contraction (the same
+    check a launch makes, raising ``LaunchError`` if it is not); a callable
+    ``lowering(prepared, target)`` replaces the whole launch of ``fn`` and is
+    the caller's responsibility."""
     if not hasattr(fn, "__hc_kernel__"):
         raise LaunchError("register_kernel() expects a function decorated with @kernel")
     if lowering == "gemm":
-        if _gemm_signature(fn) is None:
-            raise LaunchError(f"{fn.__name__} does not have a GEMM buffer signature")
-        lowering = _gemm_lowering
+        recognise(fn, Gfx950Target())
+        return fn
     if not callable(lowering):
         raise TypeError("lowering must be 'gemm' or a callable")
     _LOWERINGS[fn] = lowering
@@ -125,12 +127,14 @@ def register_kernel(fn: Any, lowering: Lowering | str = "gemm") -> Any:
 
 
 def find_lowering(fn: Any) -> Lowering:
+    """The registered lowering of ``fn``, else the GEMM if ``fn`` is the
+    tiled contraction; ``LaunchError`` otherwise."""
     lowering = _LOWERINGS.get(fn)
     if lowering is not None:
         return lowering
-    if getattr(fn, "__name__", None) in KNOWN_GEMM_KERNELS and _gemm_signature(fn) is not None:
-        return _gemm_lowering
-    raise LaunchError(f"no {TARGET_NAME} lowering for kernel {getattr(fn, '__name__', fn)!r}")
+    if not hasattr(fn, "__hc_kernel__"):
+        raise LaunchError("launch() expects a function decorated with @kernel")
+    return _contraction_lowering(recognise(fn, Gfx950Target()))
 
 
 def launch(fn: Any, *args: Any, target: Gfx950Target | None = None, **kwargs: Any) -> None:
@@ -305,8 +309,8 @@ def library_available() -> bool:
 
 __all__ = [
     "Gfx950Target",
-    "KNOWN_GEMM_KERNELS",
     "TARGET_NAME",
+    "device_available",
     "find_lowering",
     "gemm",
     "launch",

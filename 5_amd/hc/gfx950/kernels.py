@@ -6,8 +6,10 @@ intrinsic with a fallback body :144-190, verify hook :193-197, lowering hook
 :200-228, helpers :231-298, kernel :301-326) re-expressed for one 64-lane
 wavefront per 32x32 output tile and the CDNA4 instruction
 ``v_mfma_f32_32x32x16_{f16,bf16}``.  The launch does not interpret it: the
-gfx950 target lowers the whole kernel to the hand-written HIP kernels of
-libhcg_gfx950.so (256x256 macro tiles of these fragments).  The fallback body
+gfx950 target recognises the tiled contraction (statement structure plus a
+recorded CPU run through these helpers and the intrinsic's fallback body) and
+lowers the whole kernel to the hand-written HIP kernels of libhcg_gfx950.so
+(256x256 macro tiles of these fragments).  The fallback body
 states the per-lane arithmetic precisely.
 
 MFMA 32x32x16 register layout for lane l in [0, 64):
@@ -23,7 +25,7 @@ import numpy as np
 
 from ..core import Buffer, WorkGroup, WorkItem, bfloat16, kernel, vector_type
 from ..symbols import ceil_div, sym
-from . import TARGET_NAME, register_kernel
+from ._contract import TARGET_NAME
 
 WAVE_LANES = 64
 MFMA_M = 32
@@ -179,6 +181,3 @@ def tiled_gfx950_mfma_matmul_bf16(
         acc = issue_mfma_tile(group, a_tile, b_tile, acc)
     store_tile(group, c, row0, col0, acc)
 
-
-register_kernel(tiled_gfx950_mfma_matmul, "gemm")
-register_kernel(tiled_gfx950_mfma_matmul_bf16, "gemm")

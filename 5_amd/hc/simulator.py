@@ -4,14 +4,17 @@ The reference's NumPy/greenlet interpreter is not part of this build (its
 semantics are restated as a closed form in the test oracle).  ``launch``
 keeps the reference signature and routes by ``target``:
 
+* ``target=None`` uses the default target: gfx950 when the native library is
+  built and a gfx950 GPU is visible, so the reference's unchanged
+  ``sim.launch(kernel, a, b, c)`` runs on the GPU
+  (examples/amdgpu_gfx11_wmma_matmul.py:338-348); otherwise
+  ``SimulatorTarget()``.  ``HC_DEFAULT_TARGET=gfx950`` or ``=simulator``
+  forces the choice;
 * ``target=hc.gfx950.Gfx950Target(...)`` runs the kernel on gfx950;
-* ``target=None`` uses the default target, which is gfx950 when the
-  environment sets ``HC_DEFAULT_TARGET=gfx950`` (so an unchanged kernel module
-  that calls ``sim.launch(kernel, a, b, c)`` runs on the GPU), and otherwise
-  ``SimulatorTarget()``;
-* ``SimulatorTarget`` performs the full pre-launch binding and validation
-  (so ``LaunchError`` and the zero-size no-op behave as in the reference) and
-  then raises ``SimulatorError``: there is no CPU interpreter here.
+* an explicit ``SimulatorTarget`` performs the full pre-launch binding and
+  validation (so ``LaunchError`` and the zero-size no-op behave as in the
+  reference) and then raises ``SimulatorError``: there is no CPU
+  interpreter here.
 """
 
 from __future__ import annotations
@@ -38,10 +41,14 @@ DEFAULT_TARGET = SimulatorTarget()
 
 
 def default_target() -> Any:
-    if os.environ.get("HC_DEFAULT_TARGET", "").lower() in {"gfx950", "amdgpu-gfx950"}:
-        from .gfx950 import Gfx950Target
+    """The target of ``launch(..., target=None)``."""
+    choice = os.environ.get("HC_DEFAULT_TARGET", "").strip().lower()
+    if choice in {"simulator", "host"}:
+        return DEFAULT_TARGET
+    from . import gfx950
 
-        return Gfx950Target()
+    if choice in {"gfx950", "amdgpu-gfx950"} or (not choice and gfx950.device_available()):
+        return gfx950.Gfx950Target()
     return DEFAULT_TARGET
 
 
@@ -52,8 +59,8 @@ def launch(fn: Any, *args: Any, target: Any = None, **kwargs: Any) -> None:
         if prepared.is_empty:
             return
         raise SimulatorError(
-            "the host simulator is not part of this build; launch with "
-            "target=hc.gfx950.Gfx950Target() (or set HC_DEFAULT_TARGET=gfx950)"
+            "the host simulator is not part of this build; launch on a gfx950 GPU "
+            "(target=None picks it when one is visible, or target=hc.gfx950.Gfx950Target())"
         )
     from . import gfx950
 

@@ -145,14 +145,84 @@ def test_launch_requires_a_kernel_and_a_lowering():
         g.launch(_kernels.tiled_gfx950_mfma_matmul, np.zeros((4,), np.float16))
 
 
-def test_registered_kernel_gets_the_gemm_lowering():
-    g.register_kernel(_kernels.some_other_kernel)
+def test_the_reference_kernel_is_recognised_as_the_contraction():
+    from hc.gfx950 import _contract
+
+    got = _contract.recognise(_kernels.tiled_gfx11_wmma_matmul)
+    assert got.tile == (16, 16, 16) and got.dtype == "float16" and (got.a, got.b, got.c) == ("a", "b", "c")
+    assert got.intrinsics == ("wmma_gfx11",)
+    assert g.find_lowering(_kernels.tiled_gfx11_wmma_matmul).contraction == got
+
+
+def test_the_package_kernels_are_recognised_through_their_mfma_intrinsic():
+    from hc.gfx950 import _contract, kernels
+
+    for fn, dtype in ((kernels.tiled_gfx950_mfma_matmul, "float16"),
+                      (kernels.tiled_gfx950_mfma_matmul_bf16, "bfloat16")):
+        got = _contract.recognise(fn)
+        assert got.tile == (32, 32, 16) and got.dtype == dtype and got.intrinsics == ("mfma_gfx950",)
+
+
+@pytest.mark.parametrize(
+    "name,reason",
+    [
+        ("transposed_store_kernel", r"probe computes \d+ elements of c that differ from A @ B"),
+        ("k_step_32_kernel", r"K step \(32\) must equal the tiles' K extent"),
+        ("no_accumulate_kernel", "two tile loads and one accumulate"),
+        ("short_k_kernel", r"K loop must run to a.shape\[1\]"),
+        ("half_grid_kernel", r"leaves \d+ elements of c unwritten"),
+        ("unlowered_kernel", "has no lowering registered for an amdgpu target"),
+        ("some_other_kernel", "the body must be"),
+    ],
+)
+def test_near_misses_are_rejected_with_the_reason(name, reason):
+    fn = getattr(_kernels, name)
+    a, b, c = _arrays(4, 4, 4)
+    with pytest.raises(LaunchError, match=rf"no amdgpu-gfx950 lowering for kernel '{name}': .*{reason}"):
+        g.launch(fn, a, b, c, target=g.Gfx950Target())
+    with pytest.raises(LaunchError, match=reason):
+        hc.compile(fn)
+
+
+def test_a_kernel_with_the_reference_name_and_another_body_is_rejected():
+    from . import _kernels_same_name
+
+    fn = _kernels_same_name.tiled_gfx11_wmma_matmul
+    assert fn.__name__ == _kernels.tiled_gfx11_wmma_matmul.__name__
+    with pytest.raises(LaunchError, match="differ from A @ B"):
+        g.find_lowering(fn)
+    with pytest.raises(LaunchError, match="differ from A @ B"):
+        g.register_kernel(fn)
+
+
+def test_register_kernel_checks_the_body_or_takes_a_callable():
+    assert g.register_kernel(_kernels.tiled_gfx11_wmma_matmul) is _kernels.tiled_gfx11_wmma_matmul
+    with pytest.raises(LaunchError, match="the body must be"):
+        g.register_kernel(_kernels.some_other_kernel)
+    seen = []
+    g.register_kernel(_kernels.some_other_kernel, lambda prepared, target: seen.append(prepared.env))
     try:
-        assert g.find_lowering(_kernels.some_other_kernel) is g.find_lowering(_kernels.tiled_gfx11_wmma_matmul)
+        g.launch(_kernels.some_other_kernel, *_arrays(4, 5, 6))
+        assert seen and seen[0][sym.N] == 5
     finally:
         g._LOWERINGS.pop(_kernels.some_other_kernel)
-    with pytest.raises(LaunchError, match="GEMM buffer signature"):
-        g.register_kernel(_kernels.tiled_gfx950_mfma_matmul)
+
+
+def test_a_verify_hook_failure_rejects_the_kernel(monkeypatch):
+    from hc.gfx950 import _contract
+
+    def refuse(sig, target):
+        raise ValueError("not on this target")
+
+    monkeypatch.setattr(_kernels.wmma_gfx11, "__hc_verify__", refuse)
+    _contract.forget(_kernels.tiled_gfx11_wmma_matmul)
+    try:
+        with pytest.raises(LaunchError, match="verify hook failed: not on this target"):
+            g.find_lowering(_kernels.tiled_gfx11_wmma_matmul)
+    finally:
+        monkeypatch.undo()
+        _contract.forget(_kernels.tiled_gfx11_wmma_matmul)
+    assert g.find_lowering(_kernels.tiled_gfx11_wmma_matmul).contraction.tile == (16, 16, 16)
 
 
 def test_zero_size_launch_is_a_noop_on_every_target():
@@ -162,12 +232,14 @@ def test_zero_size_launch_is_a_noop_on_every_target():
 
 
 def test_simulator_target_validates_then_reports_no_interpreter(monkeypatch):
-    monkeypatch.delenv("HC_DEFAULT_TARGET", raising=False)
+    monkeypatch.setenv("HC_DEFAULT_TARGET", "simulator")
     a, b, c = _arrays(4, 4, 4)
     with pytest.raises(LaunchError, match="conflicting binding"):
         hc.simulator.launch(_kernels.tiled_gfx11_wmma_matmul, a, np.zeros((5, 4), np.float16), c)
     with pytest.raises(SimulatorError, match="host simulator is not part of this build"):
         hc.simulator.launch(_kernels.tiled_gfx11_wmma_matmul, a, b, c)
+    with pytest.raises(SimulatorError, match="host simulator is not part of this build"):
+        hc.simulator.launch(_kernels.tiled_gfx11_wmma_matmul, a, b, c, target=SimulatorTarget())
     with pytest.raises(LaunchError, match="group size exceeds"):
         hc.simulator.launch(_kernels.tiled_gfx11_wmma_matmul, a, b, c, target=SimulatorTarget(max_group_size=16))
 
@@ -175,7 +247,13 @@ def test_simulator_target_validates_then_reports_no_interpreter(monkeypatch):
 def test_default_target_switch(monkeypatch):
     monkeypatch.setenv("HC_DEFAULT_TARGET", "gfx950")
     assert isinstance(hc.simulator.default_target(), g.Gfx950Target)
-    monkeypatch.setenv("HC_DEFAULT_TARGET", "")
+    monkeypatch.setenv("HC_DEFAULT_TARGET", "simulator")
+    assert isinstance(hc.simulator.default_target(), SimulatorTarget)
+    # Unset: gfx950 exactly when a gfx950 device and the library are there.
+    monkeypatch.delenv("HC_DEFAULT_TARGET")
+    monkeypatch.setattr(g, "device_available", lambda: True)
+    assert isinstance(hc.simulator.default_target(), g.Gfx950Target)
+    monkeypatch.setattr(g, "device_available", lambda: False)
     assert isinstance(hc.simulator.default_target(), SimulatorTarget)
 
 

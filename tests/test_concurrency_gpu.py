@@ -145,14 +145,24 @@ def test_graph_capture_replays_match_eager(name, m, n, k):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=s):
         g.gemm(ta, tb, out=out)
+    # Eager calls with other operands on the capturing stream, issued so
+    # that they can overlap the replays (which run on the current stream):
+    # they must not share the scratch the graph holds.
+    a2, b2 = _inputs(name, m, n, k, seed=8)
+    ta2, tb2 = _dev(a2), _dev(b2)
+    want2 = oracle.gemm_c(a2, b2)
+    outs2 = []
     for i in range(4):
         out.fill_(float("nan"))
-        # eager work on the same stream between replays
+        torch.cuda.synchronize()
         with torch.cuda.stream(s):
-            g.gemm(ta, tb, out=torch.empty_like(out))
+            outs2.append(g.gemm(ta2, tb2))
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i}"
+    for i, o in enumerate(outs2):
+        rep = oracle.parity_check(o.cpu().numpy(), want2, k)
+        assert rep.ok, f"eager call {i}: {rep}"
 
 
 def test_graph_replays_stay_valid_after_the_stream_needs_a_larger_workspace():

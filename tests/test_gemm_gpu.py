@@ -82,6 +82,81 @@ def test_default_target_env_runs_an_unchanged_simulator_call(monkeypatch):
     _check(c, fx["c_seq"], 32)
 
 
+def test_unchanged_simulator_call_runs_on_the_gpu_without_configuration(monkeypatch):
+    """The reference driver's call, sim.launch(kernel, a, b, c) with no target
+    (examples/amdgpu_gfx11_wmma_matmul.py:338-348), on numpy inputs."""
+    import hc
+    import hc.gfx950 as g
+
+    from . import _kernels
+
+    monkeypatch.delenv("HC_DEFAULT_TARGET", raising=False)
+    assert g.device_available()
+    for name in ("ref_17x19x18_seed7", "c1_128_f16_seed0"):
+        fx = np.load(os.path.join(GOLDEN, f"{name}.npz"))
+        a, b = fx["a"], fx["b"]
+        print(f"case {name}", flush=True)
+        c = np.zeros((a.shape[0], b.shape[1]), np.float32)
+        hc.simulator.launch(_kernels.tiled_gfx11_wmma_matmul, a, b, c)
+        _check(c, fx["c_seq"], a.shape[1])
+
+
+@pytest.mark.parametrize("m,n,k", [(4095, 3001, 1027), (300, 4100, 513), (16, 8192, 8191), (4100, 4096, 256),
+                                   (1000, 33, 4096)])
+def test_plain_hcg_gemm_entry_point(m, n, k):
+    """hcg_gemm itself (not hcg_gemm_algo) with data: ragged, peeled, skinny
+    and narrow shapes, against the oracle, into a NaN guard band."""
+    from hc.gfx950 import _native
+    from hc.gfx950.workloads import make_inputs
+
+    print(f"case hcg_gemm {m}x{n}x{k}", flush=True)
+    a, b = make_inputs("c5_ragged_f16", seed=11, m=m, n=n, k=k)
+    ta, tb = _dev(a), _dev(b)
+    guard = torch.full((m + 2, n + 8), float("nan"), dtype=torch.float32, device=DEV)
+    view = guard[1 : m + 1, 4 : n + 4]
+    lib = _native.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.hcg_gemm(_native.HCG_F16, ta.data_ptr(), k, tb.data_ptr(), n, view.data_ptr(), view.stride(0), m, n, k,
+                      stream)
+    _native.check(lib, rc, "hcg_gemm")
+    torch.cuda.synchronize()
+    out = guard.cpu().numpy()
+    _check(out[1 : m + 1, 4 : n + 4], oracle.gemm_c(a, b, oracle.F16), k)
+    inner = np.zeros(out.shape, bool)
+    inner[1 : m + 1, 4 : n + 4] = True
+    assert np.isnan(out[~inner]).all(), "hcg_gemm wrote outside C"
+
+
+def test_tiled_split_override_past_16_sums_every_partial():
+    """HCG_TILED_SPLITS (read once, at the library's first call) past the
+    16 partials the vector reduce holds: 512 x 512 x 16384 in 32 K splits
+    must still sum all of K (a fresh process, so the override applies)."""
+    import subprocess
+    import sys
+    import textwrap
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    script = textwrap.dedent(f"""
+        import sys
+        sys.path[:0] = [{os.path.join(root, "5_amd")!r}, {os.path.join(root, "oracle")!r}]
+        import numpy as np, torch
+        import hc.gfx950 as g, hc_oracle as oracle
+        from hc.gfx950.workloads import make_inputs, to_torch
+        a, b = make_inputs("c5_ragged_f16", seed=21, m=512, n=500, k=16384)
+        dev = torch.device("cuda:0")
+        for n in (512, 500):  # vector reduce (N % 4 == 0) and the element reduce
+            out = g.gemm(to_torch(a, "float16", dev), to_torch(b[:, :n].copy(), "float16", dev), algo="tiled")
+            torch.cuda.synchronize()
+            rep = oracle.parity_check(out.cpu().numpy(), oracle.gemm_c(a, b[:, :n].copy()), 16384)
+            print(n, rep, flush=True)
+            assert rep.ok, rep
+    """)
+    print("case HCG_TILED_SPLITS=32 512x512x16384", flush=True)
+    env = dict(os.environ, HCG_TILED_SPLITS="32")
+    proc = subprocess.run([sys.executable, "-c", script], env=env, capture_output=True, text=True, timeout=110)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+
+
 def test_compiled_handle_launches():
     import hc
     from hc.gfx950.kernels import tiled_gfx950_mfma_matmul_bf16
