@@ -1724,6 +1724,17 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* C, int64_t ldc, i
 }
 
 
+}  // namespace
+
+// Scratch of hcg_gemm_noalloc (repacked operands and split-K partials): one
+// array per GPU, resident from the library's first use on that GPU until
+// the process ends.  In host code the name is a stand-in, not a device
+// address: the address comes from hipGetSymbolAddress, per device, at
+// set-up (DeviceState::scratch), and only that pointer is passed on.
+static __device__ __align__(256) unsigned char scratch[HCG_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -1764,6 +1775,10 @@ struct DeviceState {
   int init_status = HCG_OK;
   std::string init_error;
   int num_cus = 256;
+  // Device address of this GPU's `scratch` array (hcg_gemm_noalloc), or
+  // null with scratch_error set if the lookup failed.
+  void* scratch = nullptr;
+  std::string scratch_error;
   std::mutex ws_mutex;
   Workspace ws[kMaxStreamWorkspaces];
   int ws_next = 0;
@@ -1795,6 +1810,15 @@ int current_device_state(DeviceState** out) {
       return;
     }
     st.num_cus = cus > 0 ? cus : 256;
+    // With this device current: its copy of the scratch array.
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      st.scratch_error = std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e);
+      (void)hipGetLastError();  // the other entry points do not depend on it
+    } else {
+      st.scratch = ptr;
+    }
   });
   if (st.init_status != HCG_OK) return set_error(st.init_status, "%s", st.init_error.c_str());
   *out = &st;
@@ -2537,7 +2561,7 @@ Peel plan_peel(const DeviceState* st, const void* A, int64_t lda, const void* B,
 // stream's library workspace (nothing is allocated); null for the default.
 int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
               float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream_ptr,
-              void* fixed = nullptr, size_t fixed_bytes = 0) {
+              bool no_alloc = false) {
   if (dtype != HCG_F16 && dtype != HCG_BF16)
     return set_error(HCG_EINVAL, "dtype must be HCG_F16 (0) or HCG_BF16 (1), got %d", dtype);
   if (algo < HCG_ALGO_AUTO || algo > HCG_ALGO_NARROW)
@@ -2592,8 +2616,11 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
   Scratch sc;
   sc.st = st;
   sc.stream = stream;
-  sc.fixed = fixed;
-  sc.cap = fixed_bytes;
+  if (no_alloc) {
+    if (st->scratch == nullptr) return set_error(HCG_EHIP, "%s", st->scratch_error.c_str());
+    sc.fixed = st->scratch;
+    sc.cap = HCG_NOALLOC_SCRATCH_BYTES;
+  }
   // Workspaces stay valid while ws_mutex is held (see stream_workspace), so
   // the lock covers the launches too; a launch only enqueues work.  The two
   // launches of a peeled shape share the scratch in stream order.
@@ -2604,7 +2631,16 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
     rc = run_skinny(sc, dtype, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K);
   } else {
     const int force_shape = algo >= HCG_ALGO_TILED_256x256 ? algo - HCG_ALGO_TILED_256x256 : -1;
-    const Peel peel = algo == HCG_ALGO_AUTO ? plan_peel(st, A, lda, B, ldb, (int)M, (int)N, (int)K) : Peel{};
+    Peel peel = algo == HCG_ALGO_AUTO ? plan_peel(st, A, lda, B, ldb, (int)M, (int)N, (int)K) : Peel{};
+    // With fixed scratch, peel only when the remainder's repacked operand
+    // fits too, so that a call that cannot run fails before any launch.
+    if (sc.fixed && peel.rows > 0 &&
+        !stream_a_in_place(static_cast<const uint16_t*>(A) + (M - peel.rows) * lda, lda, peel.rows, K) &&
+        round_up((size_t)peel.rows * round_up(K, 8) * 2, 256) > sc.cap)
+      peel = Peel{};
+    if (sc.fixed && peel.cols > 0 && !(aligned16(static_cast<const uint16_t*>(B) + (N - peel.cols)) && ldb % 8 == 0) &&
+        round_up((size_t)K * round_up(peel.cols, 8) * 2, 256) > sc.cap)
+      peel = Peel{};
     if (peel.rows > 0) {
       const int mm = (int)M - peel.rows;
       rc = run_tiled(sc, dtype, A, lda, B, ldb, C, ldc, mm, (int)N, (int)K, false, -1);
@@ -2645,6 +2681,11 @@ int hcg_gemm(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, 
 int hcg_gemm_algo(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
                   float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream) {
   return gemm_impl(algo, dtype, A, lda, B, ldb, C, ldc, M, N, K, stream);
+}
+
+int hcg_gemm_noalloc(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, float* C,
+                     int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream) {
+  return gemm_impl(HCG_ALGO_AUTO, dtype, A, lda, B, ldb, C, ldc, M, N, K, stream, true);
 }
 
 const char* hcg_last_error(void) { return t_last_error.c_str(); }

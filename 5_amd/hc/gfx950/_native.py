@@ -52,8 +52,10 @@ ALGOS = {
 }
 
 # Every symbol include/hcg_gemm.h and include/hcg_tile_ops.h declare.
-EXPORTS = ("hcg_init", "hcg_gemm", "hcg_gemm_algo", "hcg_last_error", "hcg_version", "hcg_tile_load",
-           "hcg_tile_store")
+EXPORTS = ("hcg_init", "hcg_gemm", "hcg_gemm_algo", "hcg_gemm_noalloc", "hcg_last_error", "hcg_version",
+           "hcg_tile_load", "hcg_tile_store")
+
+NOALLOC_SCRATCH_BYTES = 32 << 20  # HCG_NOALLOC_SCRATCH_BYTES
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -69,6 +71,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.hcg_gemm.restype = c_int
     lib.hcg_gemm_algo.argtypes = [c_int, c_int, vp, i64, vp, i64, vp, i64, i64, i64, i64, vp]
     lib.hcg_gemm_algo.restype = c_int
+    lib.hcg_gemm_noalloc.argtypes = [c_int, vp, i64, vp, i64, vp, i64, i64, i64, i64, vp]
+    lib.hcg_gemm_noalloc.restype = c_int
     lib.hcg_last_error.argtypes = []
     lib.hcg_last_error.restype = ctypes.c_char_p
     lib.hcg_version.argtypes = []

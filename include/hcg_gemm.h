@@ -81,6 +81,25 @@ int hcg_gemm(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, 
 int hcg_gemm_algo(int algo, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
                   float* C, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* Bytes of the per-GPU scratch array behind hcg_gemm_noalloc. */
+#define HCG_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* Same as hcg_gemm, allocating nothing: no hipMalloc, hipFree or allocating
+ * library call on any path, for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid it).  No
+ * counterpart in the reference, which has no launch ABI.  Scratch
+ * (operands repacked when their rows are not 16-byte aligned, split-K
+ * partials) comes from one static device array of HCG_NOALLOC_SCRATCH_BYTES
+ * per GPU, held from the library's first use on that GPU until the process
+ * ends; K splits are limited to what fits, and a call that still needs more
+ * (large unaligned operands) fails with HCG_EINVAL before any launch.  Every
+ * call on one GPU shares that array: calls that overlap in time on one GPU
+ * (other streams, other host threads, concurrent graph replays) race, so
+ * the caller must order them.  Nothing in the array needs to start at zero:
+ * every byte a call reads was written earlier in the same call. */
+int hcg_gemm_noalloc(int dtype, const void* A, int64_t lda, const void* B, int64_t ldb, float* C,
+                     int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
+
 /* Text of the calling thread's last error ("" if none). */
 const char* hcg_last_error(void);
 
