@@ -1055,7 +1055,7 @@ __device__ __forceinline__ unsigned char* st_a() {
 __device__ __forceinline__ int sta_swz(int row, int c) { return c ^ ((row >> 2) & 3); }
 
 // UB (B's rows not 16-byte aligned, so no DMA for B): each lane fetches the
-// two aligned 16-byte blocks around its B chunk kStStages - 1 stages ahead
+// two aligned 16-byte blocks around its B chunk PF stages ahead
 // into a register set of its own, and writes the chunk (shift_join of the
 // two) just before that stage's barrier to the LDS bytes the DMA would have
 // filled.  Every lane issues two loads per chunk (the wait counts double the
@@ -1063,8 +1063,13 @@ __device__ __forceinline__ int sta_swz(int row, int c) { return c ^ ((row >> 2) 
 // block and are cleared, and a second block past B's last byte is replaced
 // by the first (its bytes reach only columns >= N).  Needs B 2-byte aligned
 // and (K - 1) * ldb + N >= 8.
-template <int DT, int R, bool UB = false>
+// PF: stages requested ahead of the one being multiplied (at most
+// kStStages - 1).  Fewer bytes in flight stream faster here: C4 (16 x 8192 x
+// 8192 fp16, B from HBM) takes 28.2 us with 7 stages ahead and 25.9 us with
+// 3; see launch_stream().
+template <int DT, int R, bool UB = false, int PF = kStStages - 1>
 __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
+  static_assert(PF >= 2 && PF < kStStages, "prefetch distance");
   static_assert(R >= 1 && R <= kStMaxRowBlocks, "row blocks");
   constexpr int NB = kStN;
   constexpr int kRowBytes = NB * 2;           // bytes per staged B row
@@ -1224,12 +1229,12 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
     }
   };
 
-  // One step from stage S: wait for it (this wave's DMAs; kStStages - 2
-  // newer stages may still be in flight), barrier (everyone's DMAs landed and
-  // everyone finished the stage being refilled), refill the previous stage
-  // with step + kStStages - 1, multiply.  Waves below R % 4 load one more A
-  // block per stage than the others.
-  constexpr int kLater = kStStages - 2;
+  // One step from stage S: wait for it (this wave's DMAs; PF - 1 newer
+  // stages may still be in flight), barrier (everyone's DMAs landed and
+  // everyone finished with stage S + PF, last read PF - kStStages steps ago),
+  // refill stage S + PF with step + PF, multiply.  Waves below R % 4 load
+  // one more A block per stage than the others.
+  constexpr int kLater = PF - 1;
   auto step_fn = [&](auto sc, int step) {
     constexpr int S = decltype(sc)::value;
     constexpr int kBLoads = UB ? 2 * kDmaPerWave : kDmaPerWave;  // B memory instructions per stage
@@ -1257,18 +1262,18 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    issue(StageC<(S + kStStages - 1) % kStStages>{}, step + kStStages - 1);
+    issue(StageC<(S + PF) % kStStages>{}, step + PF);
     compute(sc);
     __builtin_amdgcn_sched_barrier(0);
   };
 
   issue(StageC<0>{}, 0);
   issue(StageC<1>{}, 1);
-  issue(StageC<2>{}, 2);
-  issue(StageC<3>{}, 3);
-  issue(StageC<4>{}, 4);
-  issue(StageC<5>{}, 5);
-  issue(StageC<6>{}, 6);
+  if constexpr (PF > 2) issue(StageC<2>{}, 2);
+  if constexpr (PF > 3) issue(StageC<3>{}, 3);
+  if constexpr (PF > 4) issue(StageC<4>{}, 4);
+  if constexpr (PF > 5) issue(StageC<5>{}, 5);
+  if constexpr (PF > 6) issue(StageC<6>{}, 6);
 
   int step = 0;
   for (; step + kStStages <= nsteps; step += kStStages) {
@@ -2128,11 +2133,16 @@ int launch_stream(const StreamArgs& a, hipStream_t stream) {
   // mapping in gemm_stream_kernel); padding workgroups exit at once.
   const int nblocks = (a.N + kStN - 1) / kStN;
   const dim3 grid((unsigned)(round_up(nblocks, 8) * a.splits));
+  // Prefetch distance by row blocks (measured, fp16, B from HBM, us, 7 / 5 /
+  // 4 / 3 stages ahead): 16 x 8192 x 8192 28.2 / 27.6 / 26.7 / 25.9,
+  // 32 x 8192 x 8192 29.8 / 29.2 / 28.1 / 26.8, 64 x 8192 x 8192
+  // 30.1 / 29.7 / 29.5 / 29.7, 128 x 8192 x 8192 39.6 / 39.1 / 39.5 / 40.4;
+  // register-staged B (16 x 8191 x 8192) 37.5 / 36.6 / 36.0 / 35.9.
   switch (a.rblocks) {
-    case 1: gemm_stream_kernel<DT, 1, UB><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 2: gemm_stream_kernel<DT, 2, UB><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 4: gemm_stream_kernel<DT, 4, UB><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 8: gemm_stream_kernel<DT, 8, UB><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 1: gemm_stream_kernel<DT, 1, UB, 3><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 2: gemm_stream_kernel<DT, 2, UB, 3><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 4: gemm_stream_kernel<DT, 4, UB, 4><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 8: gemm_stream_kernel<DT, 8, UB, 5><<<grid, dim3(256), 0, stream>>>(a); break;
     default: return set_error(HCG_EINVAL, "internal: %d row blocks", a.rblocks);
   }
   HCG_HIP_CHECK(hipGetLastError());

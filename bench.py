@@ -27,6 +27,7 @@ metric configuration, fp16 M=N=K=4096; ``value`` is TFLOP/s
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -40,6 +41,7 @@ PEAK_F16_TFLOPS = 2516.6  # dense fp16/bf16 MFMA, MI355X
 PEAK_HBM_GBS = 8000.0
 METRIC = "TFLOP/s + % MFMA fp16 peak at 4096³ GEMM; GB/s at M=16 skinny, 1 MI355X"
 MALL_BYTES = 256 * 1024 * 1024
+LAST_ENQUEUE_S = [0.0]  # host seconds to enqueue the last timed run of launches
 
 
 def log(msg: str) -> None:
@@ -105,14 +107,25 @@ def time_launches(torch, stream, fn, steps: int, warmup: int) -> tuple[float, fl
         torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    with torch.cuda.stream(stream):
-        start.record(stream)
-        for _ in range(steps):
-            fn()
-        end.record(stream)
+    # A collection of Python's cyclic garbage collector in the middle of the
+    # enqueue loop can stall the host for tens of ms while the GPU drains its
+    # queue and idles (the events then time the idle gap too): collect now
+    # and keep the collector off until the launches are enqueued.
+    gc.collect()
+    gc.disable()
+    try:
+        t0 = time.perf_counter()
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            for _ in range(steps):
+                fn()
+            end.record(stream)
+        t_enq = time.perf_counter()
+    finally:
+        gc.enable()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    LAST_ENQUEUE_S[0] = t_enq - t0
     return start.elapsed_time(end) * 1e-3 / steps, (t1 - t0) / steps
 
 
@@ -415,7 +428,9 @@ def main() -> int:
 
     per_launch, host_per_step = time_launches(torch, stream, step, args.steps, args.warmup)
     tflops = cfg.flops / per_launch / 1e12
-    log(f"bench: {cfg.name}: {per_launch * 1e6:.1f} us/launch, {tflops:.1f} TFLOP/s")
+    enqueue_s = LAST_ENQUEUE_S[0]
+    log(f"bench: {cfg.name}: {per_launch * 1e6:.1f} us/launch, {tflops:.1f} TFLOP/s "
+        f"(host enqueue of the {args.steps} launches: {enqueue_s * 1e3:.2f} ms)")
     is_skinny = cfg.m <= 16
     kernel_name = "gemm_stream_kernel" if is_skinny else "gemm_dma_kernel"
     if is_skinny:
@@ -440,6 +455,7 @@ def main() -> int:
         "warmup": args.warmup,
         "min_warm_ms": args.min_warm_ms,
         "ms_per_step": host_per_step * 1e3,
+        "host_enqueue_ms": enqueue_s * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
