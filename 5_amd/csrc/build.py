@@ -5,7 +5,9 @@
 compiles 5_amd/csrc/hcg_gemm.hip and hcg_tile.hip (kernels + the C ABI
 declared in include/hcg_gemm.h and include/hcg_tile_ops.h) with hipcc for
 gfx950 into
-5_amd/hc/gfx950/libhcg_gfx950.so, next to the Python code that loads it.
+5_amd/hc/gfx950/libhcg_gfx950.so, next to the Python code that loads it,
+and hcg_probe.hip (the hardware ceiling probes of include/hcg_probe.h, used
+by bench.py) into 5_amd/hc/gfx950/libhcg_probe.so.
 hipcc cross-compiles, so this runs on a machine without a GPU.
 """
 
@@ -22,6 +24,8 @@ ROOT = os.path.dirname(PKG)
 SRCS = [os.path.join(HERE, "hcg_gemm.hip"), os.path.join(HERE, "hcg_tile.hip")]
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(PKG, "hc", "gfx950", "libhcg_gfx950.so")
+PROBE_SRCS = [os.path.join(HERE, "hcg_probe.hip")]
+PROBE_OUT = os.path.join(PKG, "hc", "gfx950", "libhcg_probe.so")
 ARCH = "gfx950"
 
 
@@ -49,10 +53,10 @@ def flags() -> list[str]:
     ]
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(os.path.dirname(OUT), exist_ok=True)
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), *flags(), *SRCS, "-o", tmp]
+def _compile(srcs: list[str], out: str, verbose: bool) -> str:
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + ".tmp"
+    cmd = [hipcc(), *flags(), *srcs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -64,8 +68,15 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
     if verbose and err.strip():
         print(err)
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
+    return out
+
+
+def build(verbose: bool = False) -> str:
+    """Builds the GEMM library and the probe library; returns the former."""
+    out = _compile(SRCS, OUT, verbose)
+    _compile(PROBE_SRCS, PROBE_OUT, verbose)
+    return out
 
 
 if __name__ == "__main__":

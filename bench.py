@@ -21,7 +21,14 @@ metric configuration, fp16 M=N=K=4096; ``value`` is TFLOP/s
   Infinity Cache (warm, same-buffer numbers are reported beside it);
 * ``others``: the remaining BASELINE.json configurations, TFLOP/s;
 * ``board``: graphics (per XCD too) and memory clocks and socket power
-  sampled from the driver while the headline workload runs.
+  sampled from the driver while the headline workload runs;
+* ``ceiling``: what this board sustains, measured in the same run by the
+  probes of libhcg_probe.so (include/hcg_probe.h): pure MFMA issue (TFLOP/s
+  and shader clock), streaming HBM read and write (GB/s); ``roofline`` and
+  ``skinny`` carry ``frac_of_ceiling`` beside ``frac`` (which stays against
+  the 2516.6 TFLOP/s and 8 TB/s nameplate peaks).
+
+``--ceilings-only`` runs just the probes (for rocprofv3).
 """
 
 from __future__ import annotations
@@ -58,6 +65,8 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--workload", default="c2_4096_f16")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true")
+    p.add_argument("--no-ceilings", action="store_true")
+    p.add_argument("--ceilings-only", action="store_true", help="run only the hardware ceiling probes")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU time of the baseline sample")
     p.add_argument("--profile-only", action="store_true",
                    help="run only --steps launches of the workload's GEMM (for rocprofv3), print nothing else")
@@ -401,6 +410,11 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"copy probe: 5 x {args.copy_probe} MiB device-to-device")
         return 0
+    if args.ceilings_only:
+        from hc.gfx950 import probe
+
+        print(json.dumps({"ceiling": probe.ceilings(torch, stream)}), flush=True)
+        return 0
     if args.profile_only:
         a, b = make_inputs(cfg, seed=0)
         ta, tb = to_torch(a, cfg.dtype, dev), to_torch(b, cfg.dtype, dev)
@@ -486,6 +500,19 @@ def main() -> int:
             log(f"bench: {name}")
             others[name] = bench_config(torch, g, stream, name, max(20, args.steps // 4), 5)
         result["others"] = others
+    if not args.no_ceilings:
+        log("bench: hardware ceilings (probes)")
+        from hc.gfx950 import probe
+
+        ceiling = probe.ceilings(torch, stream)
+        result["ceiling"] = ceiling
+        key, unit_key = ("hbm_read_128mib", "gbs") if is_skinny else ("mfma_f16", "tflops")
+        roofline["frac_of_ceiling"] = roofline["achieved"] / ceiling[key][unit_key]
+        roofline["ceiling_source"] = f"ceiling.{key}"
+        if "skinny" in result:
+            sk = result["skinny"]
+            sk["frac_of_ceiling"] = sk["value"] / ceiling["hbm_read_128mib"]["gbs"]
+            sk["ceiling_source"] = "ceiling.hbm_read_128mib"
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (oracle)")
         result["cpu_baseline"] = cpu_baseline(cfg, a, b, args.cpu_seconds)

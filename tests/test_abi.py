@@ -33,6 +33,26 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.hcg_version() == 100
 
 
+def test_probe_library_exports_what_its_header_declares():
+    from hc.gfx950 import probe
+
+    text = open(os.path.join(ROOT, "include", "hcg_probe.h")).read()
+    declared = sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(hcg_\w+)\s*\(", text, re.M)))
+    assert declared == sorted(probe.EXPORTS)
+    assert os.path.exists(probe.LIB_PATH), "run 5_amd/csrc/build.py"
+    lib = probe.load()
+    for name in declared:
+        assert hasattr(lib, name), name
+    # bad arguments are rejected on the host, before any launch
+    assert lib.hcg_probe_mfma(2, 1, 1, 0x1000, 0x1000, None) == 1
+    assert "dtype" in lib.hcg_probe_last_error().decode()
+    assert lib.hcg_probe_read(0x1000, 4096, 24, 8, 1, 4, 0x1000, None) == 1
+    assert "power of two" in lib.hcg_probe_last_error().decode()
+    assert lib.hcg_probe_read(0x1000, 4096, 256, 8, 1, 3, 0x1000, None) == 1
+    assert "unroll" in lib.hcg_probe_last_error().decode()
+    assert lib.hcg_probe_write(0x1000, 100, 4, 0, None) == 1
+
+
 @pytest.mark.parametrize(
     "args,match",
     [
