@@ -88,6 +88,8 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+// Four floats at a 4-byte aligned address (one 16-byte vector access).
+typedef float f32x4u __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
@@ -716,19 +718,26 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
           if (col_live) __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst));
         }
       } else {
-        // Edge tiles and C rows without 16-byte alignment: 4-byte stores,
-        // lane l at column l%32 + 32e, so each store covers 128 contiguous
-        // bytes of two rows.
+        // Edge tiles and C rows without 16-byte alignment: the same lane
+        // layout, 16-byte stores at 4-byte aligned addresses (C is float, so
+        // every address is; gfx950 takes unaligned vector stores), rows past
+        // M skipped and a chunk reaching past N stored element by element.
+        // (4-byte stores of one column per lane ran 1.4 us slower on
+        // 4095 x 3001 x 1027, whose C rows are 12004 bytes apart.)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int lr = 2 * i + (lane >> 5);
           const int grow = m0 + wm * (TM / 2) + mi * 32 + hh * 16 + lr;
+          const f32x4 v = *reinterpret_cast<const f32x4*>(ep + lr * kEpRow + c4);
+          float* dst = g.C + (int64_t)grow * g.ldc + gcol;
+          if (col_live && grow < g.M) {
+            if (gcol + 3 < g.N) {
+              *reinterpret_cast<f32x4u*>(dst) = v;
+            } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int lc = col_l + 32 * e;
-            const float v = ep[lr * kEpRow + lc];
-            const int gc = n0 + wn * (TN / 2) + lc;
-            if (lc < TN / 2 && grow < g.M && gc < g.N) g.C[(int64_t)grow * g.ldc + gc] = v;
+              for (int e = 0; e < 4; ++e)
+                if (gcol + e < g.N) dst[e] = v[e];
+            }
           }
         }
       }

@@ -155,12 +155,18 @@ run = launch
 # --------------------------------------------------------------------------
 
 
+_TORCH: Any = None
+
+
 def _torch():
-    try:
-        import torch
-    except ImportError as exc:  # pragma: no cover - torch is present on the targets
-        raise BackendError("the gfx950 backend needs PyTorch-ROCm for device memory") from exc
-    return torch
+    global _TORCH
+    if _TORCH is None:
+        try:
+            import torch
+        except ImportError as exc:  # pragma: no cover - torch is present on the targets
+            raise BackendError("the gfx950 backend needs PyTorch-ROCm for device memory") from exc
+        _TORCH = torch
+    return _TORCH
 
 
 def _check_shapes(a: Any, b: Any, c: Any | None) -> tuple[int, int, int]:
@@ -242,28 +248,44 @@ def _torch_dtype_code(torch: Any, a: Any, b: Any) -> int:
     return code
 
 
+_RAW_STREAM: Any = None
+_CUR_DEVICE: Any = None
+
+
 def _current_stream(torch: Any, index: int) -> int:
     """Raw handle of the current torch stream of device ``index``.
 
     ``torch._C._cuda_getCurrentRawStream`` returns it without building a
     ``torch.cuda.Stream`` object (a few microseconds per call); the public
     route is kept for a torch build that lacks it."""
-    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
-    if raw is not None:
-        return raw(index)
-    return torch.cuda.current_stream(index).cuda_stream
+    global _RAW_STREAM
+    if _RAW_STREAM is None:
+        _RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None) or (
+            lambda i: torch.cuda.current_stream(i).cuda_stream)
+    return _RAW_STREAM(index)
+
+
+def _current_device(torch: Any) -> int:
+    """Index of the current device (CUDA is initialised: a tensor lives
+    there).  torch._C._cuda_getDevice skips torch.cuda.current_device()'s
+    lazy-initialisation check."""
+    global _CUR_DEVICE
+    if _CUR_DEVICE is None:
+        _CUR_DEVICE = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
+    return _CUR_DEVICE()
 
 
 def _gemm_torch(torch: Any, a: Any, b: Any, out: Any | None, algo: int) -> Any:
     m, n, k = _check_shapes(a, b, out)
-    if not (a.is_cuda and b.is_cuda) or (out is not None and not out.is_cuda):
+    index = a.get_device()  # -1 on the CPU
+    ib, io = b.get_device(), (index if out is None else out.get_device())
+    if index < 0 or ib < 0 or io < 0:
         raise LaunchError("torch tensors must live on a GPU")
-    dev = a.device
-    if b.device != dev or (out is not None and out.device != dev):
+    if ib != index or io != index:
         raise LaunchError("A, B and C must live on the same device")
     dtype = _torch_dtype_code(torch, a, b)
     if out is None:
-        out = torch.empty((m, n), dtype=torch.float32, device=dev)
+        out = torch.empty((m, n), dtype=torch.float32, device=a.device)
     elif out.dtype != torch.float32:
         raise LaunchError(f"C dtype expected float32, got {str(out.dtype).replace('torch.', '')}")
     if m == 0 or n == 0:
@@ -276,15 +298,14 @@ def _gemm_torch(torch: Any, a: Any, b: Any, out: Any | None, algo: int) -> Any:
         b = b.contiguous()
         sb = b.stride()
     direct = (so[1] == 1 or n == 1) and (m == 1 or so[0] >= n)
-    target = out if direct else torch.empty((m, n), dtype=torch.float32, device=dev)
+    target = out if direct else torch.empty((m, n), dtype=torch.float32, device=a.device)
     st = so if direct else target.stride()
     # Row strides as the C ABI reads them: a one-row matrix's stride is
     # unused, so report the smallest legal one.
     lda = max(sa[0], k) if m > 1 else max(k, 1)
     ldb = max(sb[0], n) if k > 1 else max(n, 1)
     ldc = max(st[0], n) if m > 1 else max(n, 1)
-    index = dev.index if dev.index is not None else torch.cuda.current_device()
-    if torch.cuda.current_device() == index:
+    if _current_device(torch) == index:
         _native.gemm(algo, dtype, a.data_ptr(), lda, b.data_ptr(), ldb, target.data_ptr(), ldc, m, n, k,
                      _current_stream(torch, index))
     else:

@@ -12,6 +12,7 @@ dynamic loader reuses an already-loaded SONAME.
 from __future__ import annotations
 
 import ctypes
+import gc
 import os
 import threading
 
@@ -103,6 +104,15 @@ def load() -> ctypes.CDLL:
         except OSError as exc:
             raise BackendError(f"cannot load {LIB_PATH}: {exc}") from exc
         _declare(lib)
+        # The process's first full (generation 2) garbage collection after
+        # torch is imported scans ~170k objects and holds the interpreter for
+        # 40-50 ms; left alone, the few objects each call allocates trigger
+        # it a few hundred launches in, and the GPU idles while the host is
+        # stopped.  Collecting once here puts it on the first call, which
+        # already pays for loading the code object; later full collections
+        # wait for a quarter as many new long-lived objects as survive this
+        # one.
+        gc.collect()
         _lib = lib
         return lib
 

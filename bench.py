@@ -365,6 +365,34 @@ def bench_skinny(torch, g, stream, steps: int, warmup: int) -> dict:
     }
 
 
+def first_use(torch, g, stream) -> dict:
+    """Cost per call of the small C1 GEMM (128^3 fp16) from the first call
+    of this process on: the first call (it loads the library's code object
+    onto the GPU), then calls 2-100 and 101-1000, each block enqueued back
+    to back and timed on the host up to a synchronize.  Runs before any
+    other GEMM of the process."""
+    from hc.gfx950.workloads import CONFIGS, make_inputs, to_torch
+
+    cfg = CONFIGS["c1_128_f16"]
+    dev = torch.device("cuda", 0)
+    a, b = make_inputs(cfg, seed=0)
+    ta, tb = to_torch(a, cfg.dtype, dev), to_torch(b, cfg.dtype, dev)
+    tc = torch.empty((cfg.m, cfg.n), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    out = {}
+    with torch.cuda.stream(stream):
+        for label, count in (("first_call_ms", 1), ("calls_2_100_us", 99), ("calls_101_1000_us", 900)):
+            t0 = time.perf_counter()
+            for _ in range(count):
+                g.gemm(ta, tb, out=tc)
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            out[label] = dt * 1e3 if count == 1 else dt / count * 1e6
+    out["method"] = ("fresh process; host time per call of hc.gfx950.gemm on device tensors, blocks of calls "
+                     "enqueued back to back up to a synchronize")
+    return out
+
+
 def bench_config(torch, g, stream, name: str, steps: int, warmup: int) -> dict:
     from hc.gfx950.workloads import CONFIGS, make_inputs, to_torch
 
@@ -432,6 +460,7 @@ def main() -> int:
         log(f"profile-only: {args.steps} launches of {cfg.name}")
         return 0
     log(f"bench: {torch.cuda.get_device_name(0)}, workload {cfg.name}")
+    fresh = first_use(torch, g, stream) if not args.no_extra else None
 
     a, b = make_inputs(cfg, seed=0)
     ta, tb = to_torch(a, cfg.dtype, dev), to_torch(b, cfg.dtype, dev)
@@ -499,6 +528,8 @@ def main() -> int:
                 continue
             log(f"bench: {name}")
             others[name] = bench_config(torch, g, stream, name, max(20, args.steps // 4), 5)
+        if fresh is not None:
+            others["c1_128_f16"]["first_use"] = fresh
         result["others"] = others
     if not args.no_ceilings:
         log("bench: hardware ceilings (probes)")
