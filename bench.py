@@ -104,25 +104,27 @@ def time_launches(torch, stream, fn, steps: int, warmup: int) -> tuple[float, fl
     about 25 ms to settle (a 4096^3 launch takes ~165 us in the first
     milliseconds and ~115 us after), so the timed launches measure the
     sustained state."""
-    t_w = time.perf_counter()
-    with torch.cuda.stream(stream):
-        for _ in range(warmup):
-            fn()
-    torch.cuda.synchronize()
-    while time.perf_counter() - t_w < WARM_S:
-        with torch.cuda.stream(stream):
-            for _ in range(10):
-                fn()
-        torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    # A collection of Python's cyclic garbage collector in the middle of the
-    # enqueue loop can stall the host for tens of ms while the GPU drains its
-    # queue and idles (the events then time the idle gap too): collect now
-    # and keep the collector off until the launches are enqueued.
+    # A collection of Python's cyclic garbage collector can stall the host for
+    # tens of ms while the GPU drains its queue and idles: inside the timed
+    # enqueue loop the events would time that gap, and between the warm-up
+    # and the timed launches the idle board's clock drops and the first timed
+    # launches run slow.  So collect before the warm-up and keep the
+    # collector off until the timed launches are enqueued.
     gc.collect()
     gc.disable()
     try:
+        t_w = time.perf_counter()
+        with torch.cuda.stream(stream):
+            for _ in range(warmup):
+                fn()
+        torch.cuda.synchronize()
+        while time.perf_counter() - t_w < WARM_S:
+            with torch.cuda.stream(stream):
+                for _ in range(10):
+                    fn()
+            torch.cuda.synchronize()
         t0 = time.perf_counter()
         with torch.cuda.stream(stream):
             start.record(stream)
