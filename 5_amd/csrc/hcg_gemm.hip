@@ -965,12 +965,15 @@ __global__ __launch_bounds__(kSkinnyThreads) void gemm_skinny_kernel(SkinnyArgs 
 // feeds R MFMAs.  Each block's 16x32 slice of a stage arrives by one more
 // DMA instruction (block rb from wave rb % 4).
 //
-// Split-K partials go to a workspace [splits][16 R][N] and stream_reduce_kernel
-// sums them in order s = 0..S-1 (bit-reproducible).  A second launch is
-// cheaper here than an in-kernel last-arrival reduction: that needs either a
-// device-wide L2 write-back/invalidate per workgroup (agent-scope fences) or
-// L2-bypassing coherent loads, and both measured slower than the kernel
-// boundary.
+// Split-K partials go to a workspace [splits][16 R][N].  With at most
+// kStFuseMaxSplits(R) splits, R <= 2 and N a multiple of 4 the workgroups of a
+// column block reduce them themselves: each publishes its partial with
+// agent-scope (L2-coherent across XCDs) stores and counts its arrival on the
+// column block's counter; the last to arrive sums the partials in order
+// s = 0..S-1, writes C and resets the counter.  Otherwise (and for the
+// allocation-free entry point, which has no counters) stream_reduce_kernel
+// sums them in a second launch, in the same order: results are bit-identical
+// either way.
 
 constexpr int kStN = 128;
 constexpr int kStStep = 32;
@@ -979,6 +982,13 @@ constexpr int kStBBytes = kStStep * kStN * 2;  // 8 KB
 constexpr int kStABytes = 16 * kStStep * 2;    // 1 KB per 16-row block of A
 constexpr int kStMaxRowBlocks = 8;              // M <= 128
 constexpr int kStMaxSplits = 16;      // partials stream_reduce_kernel holds in registers
+// Splits the in-kernel reduction takes with R row blocks (its registers
+// hold every other split's partial; more would cost the kernel occupancy).
+constexpr int kStFuseMaxSplits(int R) { return R == 1 ? 8 : 4; }
+constexpr int kStCounterBytes = 16384;  // arrival counters ahead of each workspace: 4096 column blocks
+// Cache policy of a buffer access coherent at agent scope on gfx950 (SC1):
+// the bits the compiler gives a relaxed agent-scope atomic load or store.
+constexpr int kCpolAgent = 16;
 constexpr int kStMaxSplitsLoop = 256;  // K splits at all (more than 16: split_reduce_kernel)
 
 struct StreamArgs {
@@ -994,6 +1004,8 @@ struct StreamArgs {
   int rblocks;    // 16-row blocks of A: 1, 2, 4 or 8 (M <= 16 * rblocks)
   int a_bytes, b_bytes;
   bool c_vec;     // C rows 16-byte aligned at every 4th column
+  unsigned* counters;  // per column block arrival counters (all zero between launches), or null
+  int ws_bytes;        // bytes of the partials (with counters: below 2^31)
 };
 
 #define HCG_ST_STAGE(i) \
@@ -1062,6 +1074,98 @@ __device__ __forceinline__ unsigned char* st_a() {
 // stored at c ^ ((r >> 2) & 3), so the 16 rows read at one chunk hit 16
 // distinct 16-byte bank groups.
 __device__ __forceinline__ int sta_swz(int row, int c) { return c ^ ((row >> 2) & 3); }
+
+// The split-K reduction inside the streaming kernel (R <= 2 row blocks,
+// N % 4 == 0, splits <= kStFuseMaxSplits(R); the host checks).  Called by every
+// thread of the workgroup of (column block nb, split) after its K loop,
+// with the wave's 16x16 accumulators (register r of lane l: row 4 (l/16) + r,
+// column l%16 of the wave's column block j).
+template <int R>
+__device__ __forceinline__ void stream_fused_reduce(const StreamArgs& g, const f32x4 (&acc)[R][kStN / 64],
+                                                    int nb, int split) {
+  constexpr int NB = kStN;
+  constexpr int kColsPerWave = NB / 4;
+  constexpr int kBlocks = kColsPerWave / 16;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n0 = nb * NB;
+  // The arrival count is broadcast through B stage 7 (free after the K loop;
+  // a separate LDS variable would push two R = 2 workgroups past the CU's
+  // 160 KB).
+  unsigned* s_arrived = reinterpret_cast<unsigned*>(st_b<kStStages - 1>());
+  // Stage the 16R x 128 partial through LDS (row block rb in B stage rb:
+  // 16 x 128 floats = 8 KB), so that each thread then holds two whole
+  // 16-byte row pieces.  Every wave has finished reading the stages.
+  __syncthreads();
+#pragma unroll
+  for (int rb = 0; rb < R; ++rb) {
+    float* ep = reinterpret_cast<float*>(rb == 0 ? st_b<0>() : st_b<1>());
+#pragma unroll
+    for (int j = 0; j < kBlocks; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        ep[((lane >> 4) * 4 + r) * NB + wave * kColsPerWave + 16 * j + (lane & 15)] = acc[rb][j][r];
+  }
+  __syncthreads();
+  // Piece c (of 512 per row block): row c / 32, columns 4 (c % 32) .. +3.
+  // N % 4 == 0, so a piece is either wholly inside N or wholly past it.
+  const __amdgpu_buffer_rsrc_t rws = make_rsrc(g.ws, g.ws_bytes);
+  u32x4 mine[R][2];
+#pragma unroll
+  for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = tid + 256 * h, row = c >> 5, col = n0 + (c & 31) * 4;
+      const float* ep = reinterpret_cast<const float*>(rb == 0 ? st_b<0>() : st_b<1>());
+      mine[rb][h] = *reinterpret_cast<const u32x4*>(ep + row * NB + (c & 31) * 4);
+      if (col < g.N)
+        __builtin_amdgcn_raw_buffer_store_b128(mine[rb][h], rws,
+                                               (int)((((int64_t)split * 16 * R + 16 * rb + row) * g.N + col) * 4), 0,
+                                               kCpolAgent);
+    }
+  // The partial is visible at agent scope once its stores have completed;
+  // only then is the arrival counted.
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (tid == 0) *s_arrived = __hip_atomic_fetch_add(g.counters + nb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (*s_arrived != (unsigned)(g.splits - 1)) return;
+  // Last arrival: every other split's partial is complete.  The counter is
+  // reset for the next launch (which follows this one in stream order).
+  if (tid == 0) __hip_atomic_store(g.counters + nb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  constexpr int kMaxSplits = kStFuseMaxSplits(R);
+  u32x4 part[kMaxSplits][R][2];
+#pragma unroll
+  for (int sp = 0; sp < kMaxSplits; ++sp)
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c = tid + 256 * h, row = c >> 5, col = n0 + (c & 31) * 4;
+        part[sp][rb][h] = u32x4{0, 0, 0, 0};
+        if (sp < g.splits && sp != split && col < g.N)
+          part[sp][rb][h] = __builtin_amdgcn_raw_buffer_load_b128(
+              rws, (int)((((int64_t)sp * 16 * R + 16 * rb + row) * g.N + col) * 4), 0, kCpolAgent);
+      }
+  // Sum in split order, as stream_reduce_kernel does.
+#pragma unroll
+  for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = tid + 256 * h, row = 16 * rb + (c >> 5), col = n0 + (c & 31) * 4;
+      if (row >= g.M || col >= g.N) continue;
+      f32x4 v = __builtin_bit_cast(f32x4, split == 0 ? mine[rb][h] : part[0][rb][h]);
+#pragma unroll
+      for (int sp = 1; sp < kMaxSplits; ++sp)
+        if (sp < g.splits) v += __builtin_bit_cast(f32x4, sp == split ? mine[rb][h] : part[sp][rb][h]);
+      float* dst = g.C + (int64_t)row * g.ldc + col;
+      if (g.c_vec) {
+        *reinterpret_cast<f32x4*>(dst) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[e] = v[e];
+      }
+    }
+}
 
 // UB (B's rows not 16-byte aligned, so no DMA for B): each lane fetches the
 // two aligned 16-byte blocks around its B chunk PF stages ahead
@@ -1318,6 +1422,12 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
           if (row < g.M && col < g.N) g.C[(int64_t)row * g.ldc + col] = acc[rb][j][r];
         }
     return;
+  }
+  if constexpr (R <= 2) {
+    if (g.counters != nullptr) {
+      stream_fused_reduce<R>(g, acc, nb, split);
+      return;
+    }
   }
 #pragma unroll
   for (int rb = 0; rb < R; ++rb)
@@ -1779,9 +1889,10 @@ constexpr int kMaxStreamWorkspaces = 16;
 // hipFree, which synchronises the device.
 struct Workspace {
   void* stream = nullptr;
-  void* ptr = nullptr;
+  void* ptr = nullptr;  // kStCounterBytes of arrival counters, then `bytes` of scratch
   size_t bytes = 0;
   bool pinned = false;
+  bool counters_zeroed = false;  // the counters were cleared on this buffer's stream
 };
 
 struct DeviceState {
@@ -1842,8 +1953,12 @@ int current_device_state(DeviceState** out) {
 // The caller holds st->ws_mutex from this call until every kernel that uses
 // *out is enqueued: another thread's call (on the same stream, needing more
 // bytes, or evicting the slot) frees the buffer, and hipFree waits only for
-// work already enqueued.
-int stream_workspace(DeviceState* st, hipStream_t stream, size_t bytes, void** out) {
+// work already enqueued.  With `counters`, also returns the buffer's arrival
+// counters, first clearing them (a fill kernel on `stream`, never a memset,
+// so a capture records a kernel node) when the buffer is new or the stream
+// is being captured (a graph must not depend on what ran before a replay).
+int stream_workspace(DeviceState* st, hipStream_t stream, size_t bytes, void** out,
+                     unsigned** counters = nullptr) {
   // The null stream is never captured (and querying it during another
   // stream's capture is itself an error), so only real streams are asked.
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
@@ -1876,13 +1991,23 @@ int stream_workspace(DeviceState* st, hipStream_t stream, size_t bytes, void** o
   if (!w->ptr) {
     void* p = nullptr;
     const size_t want = bytes < ((size_t)2 << 20) ? ((size_t)2 << 20) : bytes;
-    HCG_HIP_CHECK(hipMalloc(&p, want));
+    HCG_HIP_CHECK(hipMalloc(&p, want + kStCounterBytes));
     w->ptr = p;
     w->bytes = want;
+    w->counters_zeroed = false;
   }
   w->stream = (void*)stream;
   if (capturing) w->pinned = true;
-  *out = w->ptr;
+  *out = static_cast<char*>(w->ptr) + kStCounterBytes;
+  if (counters) {
+    *counters = static_cast<unsigned*>(w->ptr);
+    if (!w->counters_zeroed || capturing) {
+      constexpr int n = kStCounterBytes / 4;
+      fill_zero_kernel<<<(n + 255) / 256, 256, 0, stream>>>(static_cast<float*>(w->ptr), n, 1, n);
+      HCG_HIP_CHECK(hipGetLastError());
+      w->counters_zeroed = true;
+    }
+  }
   return HCG_OK;
 }
 
@@ -1906,7 +2031,10 @@ struct Scratch {
   }
 };
 
-int get_scratch(const Scratch& sc, size_t bytes, void** out) {
+// `counters` (optional) receives the workspace's arrival counters, or null
+// for the fixed buffer, which has none.
+int get_scratch(const Scratch& sc, size_t bytes, void** out, unsigned** counters = nullptr) {
+  if (counters) *counters = nullptr;
   if (sc.fixed) {
     if (bytes > sc.cap)
       return set_error(HCG_EINVAL,
@@ -1916,7 +2044,7 @@ int get_scratch(const Scratch& sc, size_t bytes, void** out) {
     *out = sc.fixed;
     return HCG_OK;
   }
-  return stream_workspace(sc.st, sc.stream, bytes, out);
+  return stream_workspace(sc.st, sc.stream, bytes, out, counters);
 }
 
 // Largest split count (at most `splits`, at least 1) whose partials of
@@ -2155,7 +2283,8 @@ int launch_stream(const StreamArgs& a, hipStream_t stream) {
     default: return set_error(HCG_EINVAL, "internal: %d row blocks", a.rblocks);
   }
   HCG_HIP_CHECK(hipGetLastError());
-  if (a.splits > 1) return launch_reduce(a.ws, a.C, a.ldc, a.M, a.N, 16 * a.rblocks, a.splits, a.c_vec, stream);
+  if (a.splits > 1 && a.counters == nullptr)
+    return launch_reduce(a.ws, a.C, a.ldc, a.M, a.N, 16 * a.rblocks, a.splits, a.c_vec, stream);
   return HCG_OK;
 }
 
@@ -2222,13 +2351,23 @@ int run_skinny(const Scratch& sc, int dtype, const void* A, int64_t lda, const v
     a.b_bytes = b_dma ? (int)round_up((size_t)(((int64_t)K - 1) * ldb + N) * 2, 16) : 0;
     a.c_vec = aligned16(C) && ldc % 4 == 0;
     a.ws = nullptr;
+    a.counters = nullptr;
     // Workspace: A repacked (when it cannot be used in place), then the
     // split partials.
     const size_t p_sz = a.splits > 1 ? (size_t)a.splits * 16 * a.rblocks * (size_t)N * sizeof(float) : 0;
+    // The in-kernel reduction (see stream_fused_reduce) replaces the reduce
+    // launch: 16 x 8192 x 8192 fp16 25.9-26.0 -> 25.6-25.7 us.
+    const bool fuse = a.splits > 1 && a.rblocks <= 2 && a.splits <= kStFuseMaxSplits(a.rblocks) && N % 4 == 0 &&
+                      (N + kStN - 1) / kStN <= kStCounterBytes / 4 && p_sz < ((size_t)1 << 31);
     if (a_sz + p_sz > 0) {
       void* ws = nullptr;
-      const int rc = get_scratch(sc, a_sz + p_sz, &ws);
+      unsigned* counters = nullptr;
+      const int rc = get_scratch(sc, a_sz + p_sz, &ws, fuse ? &counters : nullptr);
       if (rc != HCG_OK) return rc;
+      if (fuse && counters) {
+        a.counters = counters;
+        a.ws_bytes = (int)p_sz;
+      }
       if (!a_in_place) {
         uint16_t* a_p = static_cast<uint16_t*>(ws);
         const RepackJob ja{a.A, lda, M, K, a_p, (int)lda_use, (int64_t)M * (lda_use / 8)};
@@ -2623,11 +2762,19 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
   // kernel, which streams B in 128-column blocks mostly past N).
   const bool use_narrow = algo == HCG_ALGO_NARROW ||
                           (algo == HCG_ALGO_AUTO && rowstream_fits(A, lda, B, ldb, M, N, K));
-  // Otherwise M <= 16, and M <= 128 where the streaming kernel applies, is
+  // Otherwise M <= 16, and M <= 64 where the streaming kernel applies, is
   // HBM-bound: B is streamed once through a skinny kernel instead of
-  // occupying only N/128 workgroups of the tiled kernel.
-  const bool use_skinny = !use_narrow && (algo == HCG_ALGO_SKINNY ||
-                                          (algo == HCG_ALGO_AUTO && (M <= 16 || stream_fits(A, lda, B, ldb, M, N, K))));
+  // occupying only N/128 workgroups of the tiled kernel.  Rows 65..128 (the
+  // streaming kernel's eight row blocks) go to the tiled kernel, which splits
+  // K to fill the chip, when B's rows are aligned (no repack of B): fp16 us,
+  // streaming -> tiled: 128^3 5.9 -> 4.4, 128 x 512 x 512 9.2 -> 6.4,
+  // 128 x 2048 x 2048 14.1 -> 11.1, 128 x 8192 x 1024 16.2 -> 9.8,
+  // 128 x 16384 x 512 17.2 -> 7.3, 128 x 8192 x 8192 38.3 -> 35.7; the
+  // streaming kernel led by at most 8% (80 x 4096 x 4096 16.6 against 18.0).
+  const bool tiled_rows = M > 64 && aligned16(B) && ldb % 8 == 0;
+  const bool use_skinny =
+      !use_narrow && (algo == HCG_ALGO_SKINNY ||
+                      (algo == HCG_ALGO_AUTO && (M <= 16 || (!tiled_rows && stream_fits(A, lda, B, ldb, M, N, K)))));
   if (algo == HCG_ALGO_NARROW && !rowstream_fits(A, lda, B, ldb, M, N, K))
     return set_error(HCG_EINVAL,
                      "the narrow kernel needs N <= 64 (and offsets of B below 2^31) "

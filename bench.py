@@ -70,6 +70,10 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU time of the baseline sample")
     p.add_argument("--profile-only", action="store_true",
                    help="run only --steps launches of the workload's GEMM (for rocprofv3), print nothing else")
+    p.add_argument("--queue-ahead", type=int, default=0, metavar="N",
+                   help="with --profile-only: afterwards, hold the GPU in a sleep kernel while N more launches "
+                        "are enqueued, so they run back to back even when the host enqueues slower than the GPU "
+                        "runs (as under a tracer), and print their event time per launch")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="run 5 device-to-device copies of MIB MiB (calibrates FETCH_SIZE/WRITE_SIZE) and exit")
     return p.parse_args()
@@ -460,6 +464,20 @@ def main() -> int:
                 g.gemm(ta, tbs[i % len(tbs)], out=tc)
         torch.cuda.synchronize()
         log(f"profile-only: {args.steps} launches of {cfg.name}")
+        if args.queue_ahead > 0:
+            # 200 us of sleep per launch to enqueue (a kernel tracer's host
+            # cost per launch is far below that), counted in shader cycles at
+            # 2.4 GHz, the highest clock: the sleep lasts at least that long.
+            n = args.queue_ahead
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(stream):
+                torch.cuda._sleep(int(n * 200e-6 * 2.4e9))
+                start.record(stream)
+                for i in range(n):
+                    g.gemm(ta, tbs[i % len(tbs)], out=tc)
+                end.record(stream)
+            torch.cuda.synchronize()
+            log(f"queued ahead: {n} launches of {cfg.name}, events {start.elapsed_time(end) * 1e3 / n:.2f} us per launch")
         return 0
     log(f"bench: {torch.cuda.get_device_name(0)}, workload {cfg.name}")
     fresh = first_use(torch, g, stream) if not args.no_extra else None

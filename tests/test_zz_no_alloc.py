@@ -68,7 +68,8 @@ PAIRS = [
     ((4095, 3001, 1027, 1027, 3001), (1000, 700, 515, 515, 700)),
     # split-K partials on the streaming kernel, then fewer rows and columns
     ((16, 8192, 8192, 8192, 8192), (16, 4096, 4096, 4096, 4096)),
-    # repacked A plus partials (M <= 128, K not a multiple of 8)
+    # repacked A plus partials (K not a multiple of 8): rows 65..128 on the
+    # tiled kernel, then 40 rows on the streaming kernel
     ((100, 6000, 8191, 8191, 6000), (40, 3000, 4001, 4001, 3000)),
     # narrow output: split partials of the narrow kernel (B repacked in the second call)
     ((6000, 40, 8192, 8192, 40), (3000, 13, 4096, 4096, 13)),
