@@ -77,63 +77,76 @@ def _bind_arguments(fn: Any, args: tuple[Any, ...], kwargs: dict[str, Any]) -> i
         raise LaunchError(f"cannot bind launch arguments: {exc}") from exc
 
 
-class _AnnotationLocals(dict):
-    """Unknown capitalised names in string annotations resolve to symbols."""
+class _SymbolFallback(dict):
+    """Evaluation namespace for string annotations: the kernel's closure
+    variables, then its globals, and any other capitalised name becomes the
+    symbol of that name (``Buffer["M", "K"]`` style annotations)."""
+
+    def __init__(self, fn: Any) -> None:
+        super().__init__(fn.__globals__)
+        self.update(inspect.getclosurevars(fn).nonlocals)
 
     def __missing__(self, name: str) -> Any:
-        if name[:1].isupper():
-            return getattr(sym, name)
-        raise KeyError(name)
+        if not name[:1].isupper():
+            raise KeyError(name)
+        return getattr(sym, name)
 
 
 def resolved_annotations(fn: Any) -> dict[str, Any]:
+    """The kernel's parameter annotations with string annotations evaluated
+    (hc/simulator.py:664-700 semantics)."""
     raw = inspect.get_annotations(fn, eval_str=False)
-    if not any(isinstance(a, str) for a in raw.values()):
+    pending = {name: text for name, text in raw.items() if isinstance(text, str)}
+    if not pending:
         return dict(raw)
-    localns = _AnnotationLocals(fn.__globals__)
-    closure = inspect.getclosurevars(fn)
-    localns.update(closure.nonlocals)
-    resolved: dict[str, Any] = {}
-    for name, annotation in raw.items():
-        if not isinstance(annotation, str):
-            resolved[name] = annotation
-            continue
+    namespace = _SymbolFallback(fn)
+    out = dict(raw)
+    for name, text in pending.items():
         try:
-            resolved[name] = eval(annotation, fn.__globals__, localns)  # noqa: S307 - annotation text
+            out[name] = eval(text, fn.__globals__, namespace)  # noqa: S307 - annotation text
         except (NameError, TypeError) as exc:
             raise LaunchError(f"failed to resolve annotations for {fn.__name__}") from exc
-    return resolved
+    return out
 
 
-def _bind_dimension(bindings: Bindings, dim: Any, value: int, source: str) -> None:
-    if isinstance(dim, Symbol):
-        bindings.bind(dim, value, source=source)
-    elif isinstance(dim, Expr):
-        bindings.require(dim, value, source=source)
-    elif isinstance(dim, int) and not isinstance(dim, bool) and dim != value:
-        raise LaunchError(f"{source} expected {dim}, got {value}")
+class _Binder:
+    """Binds observed argument extents to the symbols of their annotations,
+    raising the reference's LaunchError texts (hc/simulator.py:780-842)."""
 
+    def __init__(self) -> None:
+        self.bindings = Bindings()
 
-def _bind_buffer(bindings: Bindings, spec: BufferSpec, value: Any, source: str) -> None:
-    dtype = buffer_dtype_name(value)
-    if dtype is None:
-        raise LaunchError(f"{source} must be a numpy.ndarray or torch.Tensor buffer")
-    shape = tuple(int(d) for d in value.shape)
-    if len(shape) != len(spec.dimensions):
-        raise LaunchError(f"{source} rank does not match its Buffer annotation")
-    if spec.dtype is not None and dtype != spec.dtype:
-        raise LaunchError(f"{source} dtype expected {spec.dtype}, got {dtype}")
-    for index, dim in enumerate(spec.dimensions):
-        _bind_dimension(bindings, dim, shape[index], f"{source}.shape[{index}]")
+    def extent(self, dim: Any, value: int, where: str) -> None:
+        """One annotated extent `dim` (symbol, expression or int) observed as `value`."""
+        if isinstance(dim, Symbol):
+            self.bindings.bind(dim, value, source=where)
+        elif isinstance(dim, Expr):
+            self.bindings.require(dim, value, source=where)
+        elif isinstance(dim, int) and not isinstance(dim, bool) and dim != value:
+            raise LaunchError(f"{where} expected {dim}, got {value}")
 
+    def shape(self, dims: tuple[Any, ...], shape: tuple[int, ...], where: str) -> None:
+        for index, (dim, value) in enumerate(zip(dims, shape)):
+            self.extent(dim, int(value), f"{where}.shape[{index}]")
 
-def _bind_tuple(bindings: Bindings, dims: tuple[Any, ...], value: Any, source: str) -> None:
-    if not isinstance(value, tuple):
-        raise LaunchError(f"{source} must be a tuple")
-    if len(value) != len(dims):
-        raise LaunchError(f"{source} length does not match its tuple annotation")
-    for index, (dim, item) in enumerate(zip(dims, value)):
-        _bind_dimension(bindings, dim, int(item), f"{source}[{index}]")
+    def buffer(self, spec: BufferSpec, value: Any, where: str) -> None:
+        dtype = buffer_dtype_name(value)
+        if dtype is None:
+            raise LaunchError(f"{where} must be a numpy.ndarray or torch.Tensor buffer")
+        shape = tuple(int(d) for d in value.shape)
+        if len(shape) != len(spec.dimensions):
+            raise LaunchError(f"{where} rank does not match its Buffer annotation")
+        if spec.dtype is not None and dtype != spec.dtype:
+            raise LaunchError(f"{where} dtype expected {spec.dtype}, got {dtype}")
+        self.shape(spec.dimensions, shape, where)
+
+    def items(self, dims: tuple[Any, ...], value: Any, where: str) -> None:
+        if not isinstance(value, tuple):
+            raise LaunchError(f"{where} must be a tuple")
+        if len(value) != len(dims):
+            raise LaunchError(f"{where} length does not match its tuple annotation")
+        for index, (dim, item) in enumerate(zip(dims, value)):
+            self.extent(dim, int(item), f"{where}[{index}]")
 
 
 def _resolve_dim(value: Any, env: Env, literal_names: frozenset[str], *, static: bool, name: str) -> int:
@@ -225,14 +238,13 @@ def launch_geometry(fn: Any, shapes: dict[str, tuple[int, ...]], target: Any = N
     try:
         metadata = kernel_metadata(fn)
         annotations = resolved_annotations(fn)
-        bindings = Bindings()
+        binder = _Binder()
         for name, shape in shapes.items():
             spec = annotations.get(name)
             if not isinstance(spec, BufferSpec) or len(spec.dimensions) != len(shape):
                 raise LaunchError(f"{name} is not a Buffer of rank {len(shape)}")
-            for index, dim in enumerate(spec.dimensions):
-                _bind_dimension(bindings, dim, int(shape[index]), f"{name}.shape[{index}]")
-        return _geometry(metadata, bindings.freeze(), target)
+            binder.shape(spec.dimensions, shape, name)
+        return _geometry(metadata, binder.bindings.freeze(), target)
     except SymbolError as exc:
         raise LaunchError(str(exc)) from exc
 
@@ -242,16 +254,16 @@ def prepare_launch(fn: Any, args: tuple[Any, ...], kwargs: dict[str, Any], targe
         metadata = kernel_metadata(fn)
         bound = _bind_arguments(fn, args, kwargs)
         annotations = resolved_annotations(fn)
-        bindings = Bindings()
+        binder = _Binder()
         buffer_params: list[str] = []
         for name, value in bound.arguments.items():
             annotation = annotations.get(name, inspect.Signature.empty)
             if isinstance(annotation, BufferSpec):
-                _bind_buffer(bindings, annotation, value, name)
+                binder.buffer(annotation, value, name)
                 buffer_params.append(name)
             elif get_origin(annotation) is tuple:
-                _bind_tuple(bindings, get_args(annotation), value, name)
-        geometry = _geometry(metadata, bindings.freeze(), target)
+                binder.items(get_args(annotation), value, name)
+        geometry = _geometry(metadata, binder.bindings.freeze(), target)
     except SymbolError as exc:
         raise LaunchError(str(exc)) from exc
     return PreparedLaunch(

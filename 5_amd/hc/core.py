@@ -24,6 +24,7 @@ NumPy dtypes only).
 from __future__ import annotations
 
 import ast
+import functools
 import inspect
 import textwrap
 from collections.abc import Callable, Sequence
@@ -227,30 +228,39 @@ def _has_fallback(fn: Callable[..., Any]) -> bool:
     return not placeholder
 
 
+class _IntrinsicHooks:
+    """The per-intrinsic hook surface of hc/core.py:282-307, bound to one
+    intrinsic function: ``fn.lower(target=...)`` registers a lowering in
+    ``fn.__hc_lowerings__`` (target name -> callback), ``fn.verify`` and
+    ``fn.infer`` set ``fn.__hc_verify__`` and ``fn.__hc_infer__``; each
+    decorator returns the callback unchanged."""
+
+    def __init__(self, fn: Any) -> None:
+        self._fn = fn
+        fn.__hc_lowerings__ = {}
+        fn.__hc_verify__ = None
+        fn.__hc_infer__ = None
+        fn.__hc_has_fallback__ = _has_fallback(fn)
+
+    def lower(self, *, target: str) -> Callable[[Callable[..., Any]], Callable[..., Any]]:
+        return functools.partial(self._record_lowering, target)
+
+    def _record_lowering(self, target: str, cb: Callable[..., Any]) -> Callable[..., Any]:
+        self._fn.__hc_lowerings__[target] = cb
+        return cb
+
+    def verify(self, cb: Callable[..., Any]) -> Callable[..., Any]:
+        self._fn.__hc_verify__ = cb
+        return cb
+
+    def infer(self, cb: Callable[..., Any]) -> Callable[..., Any]:
+        self._fn.__hc_infer__ = cb
+        return cb
+
+
 def _attach_intrinsic_hooks(fn: Any) -> Any:
-    fn.__hc_lowerings__ = {}
-    fn.__hc_verify__ = None
-    fn.__hc_infer__ = None
-    fn.__hc_has_fallback__ = _has_fallback(fn)
-
-    def lower(*, target: str) -> Callable[[Callable[..., Any]], Callable[..., Any]]:
-        def register(cb: Callable[..., Any]) -> Callable[..., Any]:
-            fn.__hc_lowerings__[target] = cb
-            return cb
-
-        return register
-
-    def verify(cb: Callable[..., Any]) -> Callable[..., Any]:
-        fn.__hc_verify__ = cb
-        return cb
-
-    def infer(cb: Callable[..., Any]) -> Callable[..., Any]:
-        fn.__hc_infer__ = cb
-        return cb
-
-    fn.lower = lower
-    fn.verify = verify
-    fn.infer = infer
+    hooks = _IntrinsicHooks(fn)
+    fn.lower, fn.verify, fn.infer = hooks.lower, hooks.verify, hooks.infer
     return fn
 
 
@@ -351,54 +361,33 @@ class CurrentGroup:
     def workitems(self, fn: Callable[..., Any]) -> Callable[..., Any]:
         return fn
 
-    def _runtime(self, name: str) -> Any:
-        raise NotImplementedError(f"{name} is implemented by runtime backends")
-
-    def barrier(self) -> None:
-        self._runtime("barrier")
-
-    def load(self, *args: Any, **kwargs: Any) -> Any:
-        return self._runtime("load")
-
-    def vload(self, *args: Any, **kwargs: Any) -> Any:
-        return self._runtime("vload")
-
-    def store(self, *args: Any, **kwargs: Any) -> Any:
-        return self._runtime("store")
-
-    def empty(self, *args: Any, **kwargs: Any) -> Any:
-        return self._runtime("empty")
-
-    def zeros(self, *args: Any, **kwargs: Any) -> Any:
-        return self._runtime("zeros")
-
-    def ones(self, *args: Any, **kwargs: Any) -> Any:
-        return self._runtime("ones")
-
-    def full(self, *args: Any, **kwargs: Any) -> Any:
-        return self._runtime("full")
-
-    def vzeros(self, *args: Any, **kwargs: Any) -> Any:
-        return self._runtime("vzeros")
-
-    def vones(self, *args: Any, **kwargs: Any) -> Any:
-        return self._runtime("vones")
-
-    def vfull(self, *args: Any, **kwargs: Any) -> Any:
-        return self._runtime("vfull")
-
 
 class SubGroup:
-    def subgroup_id(self) -> int:
-        raise NotImplementedError("subgroup_id is implemented by runtime backends")
-
-    def size(self) -> int:
-        raise NotImplementedError("size is implemented by runtime backends")
+    """A subgroup's view inside a kernel (``subgroup_id()``, ``size()``); only a
+    runtime gives the methods meaning."""
 
 
 class WorkItem:
-    def global_id(self) -> tuple[int, ...]:
-        raise NotImplementedError("global_id is implemented by runtime backends")
+    """A work item's view inside a kernel (``global_id()``, ``local_id()``);
+    only a runtime gives the methods meaning."""
 
-    def local_id(self) -> tuple[int, ...]:
-        raise NotImplementedError("local_id is implemented by runtime backends")
+
+def _outside_launch(owner: str, name: str) -> Callable[..., Any]:
+    def method(self: Any, *args: Any, **kwargs: Any) -> Any:
+        raise NotImplementedError(
+            f"{owner}.{name}() means something only while a kernel runs: launch it with "
+            "hc.simulator.launch, hc.gfx950.launch or hc.compile(kernel)(...)")
+
+    method.__name__ = method.__qualname__ = name
+    return method
+
+
+for _owner, _cls, _names in (
+    ("group", CurrentGroup, ("barrier", "load", "vload", "store", "empty", "zeros", "ones", "full", "vzeros",
+                             "vones", "vfull")),
+    ("subgroup", SubGroup, ("subgroup_id", "size")),
+    ("workitem", WorkItem, ("global_id", "local_id")),
+):
+    for _name in _names:
+        setattr(_cls, _name, _outside_launch(_owner, _name))
+del _owner, _cls, _names, _name
