@@ -410,7 +410,16 @@ __device__ __forceinline__ int b_chunk_swz(int k, int c) {
 // (B: at the end of the chunk holding it), so every offset stays small; the
 // range check still zero-fills rows past M and K, and chunks past N are
 // redirected past the extent.
-template <int DT, int TM, int TN, int STAGES, bool WIDE = false>
+//
+// KT: A is read in place with K not a multiple of 8, so the chunk holding
+// column K - 1 also brings up to 7 elements past K (the next row or row
+// padding, possibly Inf or NaN), which would meet B's zero-filled rows past
+// K.  The fragments of the tile holding K - 1 are masked: those elements
+// become +0.  (The DMA reads 16-byte chunks at any 2-byte alignment, so
+// operands with unaligned rows are read in place; the host checks that the
+// bytes a last chunk reads past an operand's end stay in the page of its
+// last element.)
+template <int DT, int TM, int TN, int STAGES, bool WIDE = false, bool KT = false>
 __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_kernel(FastArgs g) {
   static_assert((TM == 256 && STAGES == 4) || (TM == 128 && STAGES == 3), "tile variant");
   static_assert(TN == 256 || TN == 192 || TN == 128 || TN == 64, "tile width");
@@ -471,6 +480,12 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
     const int c = a_chunk_swz(row, lane & 3);
     a_col[i] = c * 8;
     a_off[i] = ((a_row0 + row) * g.lda + c * 8) * 2;
+    // KT: rows past M start at the extent, so that they read zeros whatever
+    // the K advance (with rows of fewer than round_up(K, 8) elements, which
+    // only K % 8 != 0 allows, row M's first chunk would otherwise lie partly
+    // inside it).
+    if constexpr (KT && !WIDE)
+      if (m0 + row >= g.M) a_off[i] = g.a_bytes;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -570,6 +585,19 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
     }
   };
 
+  // KT: clear the A fragment elements at k >= K of 16-wide K step kk of
+  // tile kt (a lane's fragment holds 8 consecutive k of one row; word w
+  // holds elements 2w and 2w + 1).
+  auto mask_tail = [&](u32x4 (&fa)[kMi], int kt, int kk) {
+    const int v = min(max(g.K - (kt * kDmaK + kk * 16 + (lane >> 5) * 8), 0), 8);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t m = (2 * w < v ? 0x0000ffffu : 0u) | (2 * w + 1 < v ? 0xffff0000u : 0u);
+#pragma unroll
+      for (int mi = 0; mi < kMi; ++mi) fa[mi][w] &= m;
+    }
+  };
+
   f32x16 acc[kMi][kNi];
 #pragma unroll
   for (int i = 0; i < kMi; ++i)
@@ -618,7 +646,10 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
   // past K load zeros and are never multiplied.
   auto iteration = [&](auto sc, auto full, int kt) {
     constexpr int S = decltype(sc)::value;
+    // (Tiles read by full iterations lie wholly inside K: no tail mask.)
+    constexpr bool kMask = KT && !decltype(full)::value;
     read_frags(sc, 1, fa1, fb1);
+    if constexpr (kMask) mask_tail(fa1, kt, 1);
     issue_b(StageC<(S + STAGES - 1) % STAGES>{}, full, kt + STAGES - 1);
     mfma_block(fa0, fb0);
     schedule(std::integral_constant<int, 4>{});
@@ -631,6 +662,7 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
     __builtin_amdgcn_sched_barrier(0);
     // Every wave is past its reads of tile kt: stage S takes tile kt+STAGES.
     read_frags(StageC<(S + 1) % STAGES>{}, 0, fa0, fb0);
+    if constexpr (kMask) mask_tail(fa0, kt + 1, 0);
     issue_a(sc, full, kt + STAGES);
     mfma_block(fa1, fb1);
     schedule(std::integral_constant<int, kADma>{});
@@ -651,6 +683,7 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   read_frags(StageC<0>{}, 0, fa0, fb0);
+  if constexpr (KT) mask_tail(fa0, 0, 0);
 
   using Full = std::true_type;
   using Checked = std::false_type;
@@ -2186,16 +2219,16 @@ TilePlan plan_tiles(int num_cus, int M, int N, int K, int force_shape, bool allo
 }
 
 
-template <int DT, bool WIDE>
+template <int DT, bool WIDE, bool KT = false>
 int launch_dma(const FastArgs& a, int shape, hipStream_t stream) {
   const dim3 grid((unsigned)(a.tiles_m * a.tiles_n * (a.splits > 1 ? a.splits : 1)));
   const dim3 block(kTiledThreads);
   switch (shape) {
-    case 0: gemm_dma_kernel<DT, 256, 256, 4, WIDE><<<grid, block, 0, stream>>>(a); break;
-    case 1: gemm_dma_kernel<DT, 256, 192, 4, WIDE><<<grid, block, 0, stream>>>(a); break;
-    case 2: gemm_dma_kernel<DT, 128, 256, 3, WIDE><<<grid, block, 0, stream>>>(a); break;
-    case 3: gemm_dma_kernel<DT, 128, 128, 3, WIDE><<<grid, block, 0, stream>>>(a); break;
-    default: gemm_dma_kernel<DT, 256, 64, 4, WIDE><<<grid, block, 0, stream>>>(a); break;
+    case 0: gemm_dma_kernel<DT, 256, 256, 4, WIDE, KT><<<grid, block, 0, stream>>>(a); break;
+    case 1: gemm_dma_kernel<DT, 256, 192, 4, WIDE, KT><<<grid, block, 0, stream>>>(a); break;
+    case 2: gemm_dma_kernel<DT, 128, 256, 3, WIDE, KT><<<grid, block, 0, stream>>>(a); break;
+    case 3: gemm_dma_kernel<DT, 128, 128, 3, WIDE, KT><<<grid, block, 0, stream>>>(a); break;
+    default: gemm_dma_kernel<DT, 256, 64, 4, WIDE, KT><<<grid, block, 0, stream>>>(a); break;
   }
   HCG_HIP_CHECK(hipGetLastError());
   return HCG_OK;
@@ -2554,18 +2587,38 @@ int64_t fast_extent_b(int N, int K, int64_t ldb) {
   return ((int64_t)round_up(K, kTileK) * ldb + round_up(N, kTileN) + 8) * 2;
 }
 
+// True when the bytes from an operand's last element (row rows - 1, column
+// cols - 1, row stride ld, 16-bit elements) to 16 bytes past the end of the
+// 8-element chunk that holds it lie in one 4 KB page.  The DMA kernel reads
+// whole chunks, so with rows that are not 16-byte aligned it reads up to 14
+// bytes past an operand's last element; within that element's page no read
+// can touch an unmapped page.
+bool chunk_tail_in_page(const void* base, int64_t rows, int64_t cols, int64_t ld) {
+  const uintptr_t p = reinterpret_cast<uintptr_t>(base);
+  const uintptr_t last = p + (uintptr_t)(((rows - 1) * ld + cols) * 2) - 1;
+  const uintptr_t end = p + (uintptr_t)(((rows - 1) * ld + (int64_t)round_up(cols, 8)) * 2) + 16;
+  return (last >> 12) == ((end - 1) >> 12);
+}
+
 int run_tiled(const Scratch& sc, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
               float* C, int64_t ldc, int M, int N, int K, bool force_generic, int force_shape) {
   DeviceState* st = sc.st;
   hipStream_t stream = sc.stream;
   const int64_t kLimit = (int64_t)1 << 31;
-  // The DMA kernel masks at 8-element granularity.  A also needs K a
-  // multiple of 8 (or zero padding supplied by a repack): a chunk straddling
-  // K would pair A's row padding, possibly Inf or NaN, with zeroed B rows.
-  // B's chunk straddling N reads padding columns (in the same 16 bytes as
-  // column N - 1) that reach only C columns >= N, which are never stored.
-  const bool a_ok = aligned16(A) && lda % 8 == 0 && K % 8 == 0;
-  const bool b_ok = aligned16(B) && ldb % 8 == 0;
+  // The DMA kernel moves 16-byte chunks (8 elements) at any 2-byte
+  // alignment, so operands are read in place whenever the last chunk's
+  // bytes past the operand stay in its last page (chunk_tail_in_page);
+  // otherwise they are repacked into zero-padded aligned rows.  A chunk of A
+  // straddling K brings elements past K (the next row or row padding), which
+  // the kernel clears (KT); B's chunk straddling N brings columns past N,
+  // which reach only C columns >= N, never stored.
+  const bool a_aligned = aligned16(A) && lda % 8 == 0 && K % 8 == 0;
+  const bool b_aligned = aligned16(B) && ldb % 8 == 0;
+  const bool a_ok = a_aligned || (K > 0 && (reinterpret_cast<uintptr_t>(A) & 1) == 0 &&
+                                  chunk_tail_in_page(A, M, K, lda));
+  const bool b_ok = b_aligned || (N > 0 && (reinterpret_cast<uintptr_t>(B) & 1) == 0 &&
+                                  chunk_tail_in_page(B, K, N, ldb));
+  const bool k_tail = a_ok && K % 8 != 0;
   const int64_t lda_p = a_ok ? lda : (int64_t)round_up(K, 8);
   const int64_t ldb_p = b_ok ? ldb : (int64_t)round_up(N, 8);
   const int64_t tiles = (int64_t)((M + kTileM - 1) / kTileM) * ((N + kTileN - 1) / kTileN);
@@ -2574,7 +2627,7 @@ int run_tiled(const Scratch& sc, int dtype, const void* A, int64_t lda, const vo
   // Aligned operands too large for 32-bit offsets from their base run the
   // WIDE form (per-tile / per-K-tile resources) when one 256-row panel of A
   // and one 32-row panel of B stay below 2^31 bytes.
-  const bool wide = !fits && a_ok && b_ok && (int64_t)kTileM * lda * 2 < kLimit &&
+  const bool wide = !fits && a_aligned && b_aligned && (int64_t)kTileM * lda * 2 < kLimit &&
                     (int64_t)kDmaK * ldb * 2 < kLimit && tiles <= 0x7fffffff;
   if (force_generic || (!fits && !wide)) return run_generic(dtype, A, lda, B, ldb, C, ldc, M, N, K, stream);
   if (wide) {
@@ -2645,10 +2698,10 @@ int run_tiled(const Scratch& sc, int dtype, const void* A, int64_t lda, const vo
   f.K = K;
   f.tiles_m = (M + ts.tm - 1) / ts.tm;
   f.tiles_n = (N + ts.tn - 1) / ts.tn;
-  // Range-check extents cover the last valid element, rounded up to the
-  // 16-byte chunk that holds it (never past that chunk).
-  f.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda_p + K) * 2, 16);
-  f.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * ldb_p + N) * 2, 16);
+  // Range-check extents cover the chunk that holds the last valid element
+  // (never past that chunk).
+  f.a_bytes = (int)((((int64_t)M - 1) * lda_p + (int64_t)round_up(K, 8)) * 2);
+  f.b_bytes = (int)((((int64_t)K - 1) * ldb_p + (int64_t)round_up(N, 8)) * 2);
   f.c_vec = aligned16(C) && ldc % 4 == 0;
   f.splits = 1;
   if (plan.splits > 1) {
@@ -2659,8 +2712,10 @@ int run_tiled(const Scratch& sc, int dtype, const void* A, int64_t lda, const vo
     f.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + a_sz + b_sz);
     f.ws_vec = N % 4 == 0;  // 16-byte partial rows (the workspace base is 256-byte aligned)
   }
-  const int rc = dtype == HCG_F16 ? launch_dma<HCG_F16, false>(f, plan.shape, stream)
-                                  : launch_dma<HCG_BF16, false>(f, plan.shape, stream);
+  const int rc = k_tail ? (dtype == HCG_F16 ? launch_dma<HCG_F16, false, true>(f, plan.shape, stream)
+                                          : launch_dma<HCG_BF16, false, true>(f, plan.shape, stream))
+                        : (dtype == HCG_F16 ? launch_dma<HCG_F16, false>(f, plan.shape, stream)
+                                            : launch_dma<HCG_BF16, false>(f, plan.shape, stream));
   if (rc != HCG_OK || f.splits == 1) return rc;
   return launch_reduce(f.ws, C, ldc, M, N, M, f.splits, aligned16(C) && ldc % 4 == 0, stream);
 }

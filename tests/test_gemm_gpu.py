@@ -650,6 +650,70 @@ def test_unaligned_strided_views_against_oracle(m, n, k, pad_a, pad_b):
     assert np.all(np.isnan(host[mask]))
 
 
+# Rows that are not 16-byte aligned are read in place by the tiled kernel's
+# DMA (16-byte chunks at 2-byte alignment).  The chunk of A holding column
+# K - 1 also brings up to 7 elements past K: row padding (here +Inf, so an
+# uncleared element would turn a product with B's zeroed rows into NaN) or,
+# for tight rows, the next row.
+@pytest.mark.parametrize(
+    "m,n,k,pad_a,pad_b,algo,dtype",
+    [
+        (4095, 3001, 1027, 0, 0, "auto", "float16"),
+        (601, 713, 1027, 9, 3, "tiled_256x192", "float16"),
+        (333, 270, 150, 1, 1, "tiled_128x128", "bfloat16"),
+        (300, 1000, 8195, 3, 5, "auto", "float16"),
+        (257, 129, 31, 7, 0, "tiled_256x256", "bfloat16"),
+        (64, 200, 13, 3, 3, "tiled_128x256", "float16"),
+        (700, 64, 2049, 5, 1, "tiled_256x64", "float16"),
+    ],
+)
+def test_unaligned_rows_read_in_place(m, n, k, pad_a, pad_b, algo, dtype):
+    import hc.gfx950 as g
+
+    rng = np.random.default_rng(m + 3 * n + 7 * k)
+    ai = rng.integers(-4, 5, size=(m, k))
+    bi = rng.integers(-4, 5, size=(k, n))
+    tdt = torch.float16 if dtype == "float16" else torch.bfloat16
+    big_a = torch.full((m, k + pad_a), float("inf"), dtype=tdt, device=DEV)
+    big_b = torch.full((k, n + pad_b), float("inf"), dtype=tdt, device=DEV)
+    va, vb = big_a[:, :k], big_b[:, :n]
+    va.copy_(torch.from_numpy(ai).to(DEV, tdt))
+    vb.copy_(torch.from_numpy(bi).to(DEV, tdt))
+    guard = torch.full((m + 2, n + 3), float("nan"), dtype=torch.float32, device=DEV)
+    vc = guard[1 : m + 1, 1 : n + 1]
+    print(f"case in-place unaligned {algo} {dtype} m={m} n={n} k={k} pad_a={pad_a} pad_b={pad_b}", flush=True)
+    g.gemm(va, vb, out=vc, algo=algo)
+    torch.cuda.synchronize()
+    host = guard.cpu().numpy()
+    assert np.array_equal(host[1 : m + 1, 1 : n + 1], (ai @ bi).astype(np.float32))
+    mask = np.ones_like(host, dtype=bool)
+    mask[1 : m + 1, 1 : n + 1] = False
+    assert np.all(np.isnan(host[mask]))
+
+
+def test_unaligned_rows_whose_last_chunk_crosses_a_page_are_repacked():
+    """An A view placed so that its last element ends a 4 KB page: the DMA
+    would read past it into the next page, so the library repacks A instead;
+    the result is the same."""
+    import hc.gfx950 as g
+
+    m, n, k = 300, 200, 1027  # K % 8 == 3: the last chunk reads 10 bytes past A's end
+    rng = np.random.default_rng(77)
+    ai = rng.integers(-4, 5, size=(m, k))
+    bi = rng.integers(-4, 5, size=(k, n))
+    buf = torch.zeros(m * k + 8192, dtype=torch.float16, device=DEV)
+    last = buf.data_ptr() + 2 * (m * k - 1)  # last element's address for a view at offset 0
+    off = ((4094 - last % 4096) % 4096) // 2  # move the view so that it ends on a page's last 2 bytes
+    va = buf[off : off + m * k].view(m, k)
+    assert (va.data_ptr() + 2 * (m * k) - 1) % 4096 == 4095
+    va.copy_(torch.from_numpy(ai).to(DEV, torch.float16))
+    vb = torch.from_numpy(bi).to(DEV, torch.float16)
+    print("case page-crossing tail repacked", flush=True)
+    out = g.gemm(va, vb)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), (ai @ bi).astype(np.float32))
+
+
 @pytest.mark.parametrize("algo", ["auto"] + TILE_ALGOS)
 def test_strided_views_and_guard_band(algo):
     """A and B as column-sliced views (lda > K, ldb > N, 2-byte aligned
