@@ -1947,10 +1947,15 @@ DeviceState g_devices[kMaxDevices];
 std::once_flag g_global_once;
 int g_skinny_splits_override = 0;
 int g_tiled_splits_override = 0;  // HCG_TILED_SPLITS: split count for the tiled kernel, if valid
+// HCG_UNALIGNED_DMA=0: never read rows that are not 16-byte aligned in place
+// (repack or register-stage them, the paths for operands the DMA cannot
+// read); for tests of those paths.
+bool g_unaligned_dma = true;
 
 void global_init() {
   if (const char* s = getenv("HCG_SKINNY_SPLITS")) g_skinny_splits_override = atoi(s);
   if (const char* s = getenv("HCG_TILED_SPLITS")) g_tiled_splits_override = atoi(s);
+  if (const char* s = getenv("HCG_UNALIGNED_DMA")) g_unaligned_dma = atoi(s) != 0;
 }
 
 int current_device_state(DeviceState** out) {
@@ -2046,6 +2051,31 @@ int stream_workspace(DeviceState* st, hipStream_t stream, size_t bytes, void** o
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// True when the DMA may read the whole 8-element chunk that holds an
+// operand's last element (row rows - 1, column cols - 1, row stride ld,
+// 16-bit elements) and 16 bytes more: with rows that are not 16-byte
+// aligned the DMA kernels read up to 14 bytes past an operand's last
+// element.  Those bytes are safe when they lie in the last element's 4 KB
+// page, or inside the device allocation that holds the operand (a tight
+// operand of a whole number of pages ends exactly at a page boundary).
+bool chunk_tail_readable(const void* base, int64_t rows, int64_t cols, int64_t ld) {
+  if (!g_unaligned_dma) return false;
+  const uintptr_t p = reinterpret_cast<uintptr_t>(base);
+  const uintptr_t last = p + (uintptr_t)(((rows - 1) * ld + cols) * 2) - 1;
+  const uintptr_t end = p + (uintptr_t)(((rows - 1) * ld + (int64_t)round_up(cols, 8)) * 2) + 16;
+  if ((last >> 12) == ((end - 1) >> 12)) return true;
+  hipDeviceptr_t alloc = nullptr;
+  size_t alloc_bytes = 0;
+  if (hipMemGetAddressRange(&alloc, &alloc_bytes, const_cast<void*>(base)) != hipSuccess) {
+    (void)hipGetLastError();  // not device memory of this process: stay on the safe side
+    return false;
+  }
+  return end <= reinterpret_cast<uintptr_t>(alloc) + alloc_bytes;
+}
+
+// 16-bit operands: any element address is 2-byte aligned.
+bool aligned2(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
 
 // Where a call's scratch comes from: its stream's library workspace
 // (allocated on demand, see stream_workspace), or a fixed device buffer of
@@ -2335,12 +2365,18 @@ int stream_rblocks(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 :
 bool stream_extent_a(int64_t lda, int64_t M, int64_t K) {
   return ((int64_t)16 * stream_rblocks(M) * lda + K) * 2 < ((int64_t)1 << 31);
 }
+// The DMA reads 16-byte chunks at any 2-byte alignment: rows that are not
+// 16-byte aligned are read in place when the last chunk's bytes past the
+// operand stay in its last page (chunk_tail_readable).  A also needs K a
+// multiple of 8 (no chunk of A straddles K: this kernel does not clear
+// elements past K).
 bool stream_a_in_place(const void* A, int64_t lda, int64_t M, int64_t K) {
-  return aligned16(A) && lda % 8 == 0 && K % 8 == 0 && stream_extent_a(lda, M, K);
+  return K % 8 == 0 && stream_extent_a(lda, M, K) &&
+         ((aligned16(A) && lda % 8 == 0) || (aligned2(A) && chunk_tail_readable(A, M, K, lda)));
 }
 bool stream_b_dma(const void* B, int64_t ldb, int64_t N, int64_t K) {
-  return aligned16(B) && ldb % 8 == 0 &&
-         ((int64_t)round_up(K, kStStep) * ldb + round_up(N, kStN)) * 2 < ((int64_t)1 << 31);
+  return ((int64_t)round_up(K, kStStep) * ldb + round_up(N, kStN)) * 2 < ((int64_t)1 << 31) &&
+         ((aligned16(B) && ldb % 8 == 0) || (aligned2(B) && chunk_tail_readable(B, K, N, ldb)));
 }
 // B that the DMA cannot take (rows not 16-byte aligned, or offsets past
 // 2^31) is register-staged: 16-byte loads at any 2-byte alignment, all
@@ -2379,9 +2415,10 @@ int run_skinny(const Scratch& sc, int dtype, const void* A, int64_t lda, const v
     a.kchunk = ((ksteps + a.splits - 1) / a.splits) * kStStep;
     a.splits = (K + a.kchunk - 1) / a.kchunk;  // drop empty trailing splits
     a.rblocks = stream_rblocks(M);
-    a.a_bytes = (int)round_up((size_t)(((int64_t)M - 1) * lda_use + K) * 2, 16);
+    // Extents end with the chunk that holds the last element.
+    a.a_bytes = (int)((((int64_t)M - 1) * lda_use + (int64_t)round_up(K, 8)) * 2);
     // (register-staged B reads through plain pointers: no extent)
-    a.b_bytes = b_dma ? (int)round_up((size_t)(((int64_t)K - 1) * ldb + N) * 2, 16) : 0;
+    a.b_bytes = b_dma ? (int)((((int64_t)K - 1) * ldb + (int64_t)round_up(N, 8)) * 2) : 0;
     a.c_vec = aligned16(C) && ldc % 4 == 0;
     a.ws = nullptr;
     a.counters = nullptr;
@@ -2587,19 +2624,6 @@ int64_t fast_extent_b(int N, int K, int64_t ldb) {
   return ((int64_t)round_up(K, kTileK) * ldb + round_up(N, kTileN) + 8) * 2;
 }
 
-// True when the bytes from an operand's last element (row rows - 1, column
-// cols - 1, row stride ld, 16-bit elements) to 16 bytes past the end of the
-// 8-element chunk that holds it lie in one 4 KB page.  The DMA kernel reads
-// whole chunks, so with rows that are not 16-byte aligned it reads up to 14
-// bytes past an operand's last element; within that element's page no read
-// can touch an unmapped page.
-bool chunk_tail_in_page(const void* base, int64_t rows, int64_t cols, int64_t ld) {
-  const uintptr_t p = reinterpret_cast<uintptr_t>(base);
-  const uintptr_t last = p + (uintptr_t)(((rows - 1) * ld + cols) * 2) - 1;
-  const uintptr_t end = p + (uintptr_t)(((rows - 1) * ld + (int64_t)round_up(cols, 8)) * 2) + 16;
-  return (last >> 12) == ((end - 1) >> 12);
-}
-
 int run_tiled(const Scratch& sc, int dtype, const void* A, int64_t lda, const void* B, int64_t ldb,
               float* C, int64_t ldc, int M, int N, int K, bool force_generic, int force_shape) {
   DeviceState* st = sc.st;
@@ -2607,17 +2631,15 @@ int run_tiled(const Scratch& sc, int dtype, const void* A, int64_t lda, const vo
   const int64_t kLimit = (int64_t)1 << 31;
   // The DMA kernel moves 16-byte chunks (8 elements) at any 2-byte
   // alignment, so operands are read in place whenever the last chunk's
-  // bytes past the operand stay in its last page (chunk_tail_in_page);
+  // bytes past the operand stay in its last page (chunk_tail_readable);
   // otherwise they are repacked into zero-padded aligned rows.  A chunk of A
   // straddling K brings elements past K (the next row or row padding), which
   // the kernel clears (KT); B's chunk straddling N brings columns past N,
   // which reach only C columns >= N, never stored.
   const bool a_aligned = aligned16(A) && lda % 8 == 0 && K % 8 == 0;
   const bool b_aligned = aligned16(B) && ldb % 8 == 0;
-  const bool a_ok = a_aligned || (K > 0 && (reinterpret_cast<uintptr_t>(A) & 1) == 0 &&
-                                  chunk_tail_in_page(A, M, K, lda));
-  const bool b_ok = b_aligned || (N > 0 && (reinterpret_cast<uintptr_t>(B) & 1) == 0 &&
-                                  chunk_tail_in_page(B, K, N, ldb));
+  const bool a_ok = a_aligned || (K > 0 && aligned2(A) && chunk_tail_readable(A, M, K, lda));
+  const bool b_ok = b_aligned || (N > 0 && aligned2(B) && chunk_tail_readable(B, K, N, ldb));
   const bool k_tail = a_ok && K % 8 != 0;
   const int64_t lda_p = a_ok ? lda : (int64_t)round_up(K, 8);
   const int64_t ldb_p = b_ok ? ldb : (int64_t)round_up(N, 8);

@@ -108,11 +108,11 @@ def load() -> ctypes.CDLL:
         # torch is imported scans ~170k objects and holds the interpreter for
         # 40-50 ms; left alone, the few objects each call allocates trigger
         # it a few hundred launches in, and the GPU idles while the host is
-        # stopped.  Collecting once here puts it on the first call, which
-        # already pays for loading the code object; later full collections
-        # wait for a quarter as many new long-lived objects as survive this
-        # one.
-        gc.collect()
+        # stopped.  Freezing the objects that exist now (the imported modules
+        # and their data, which live for the whole process) takes them out
+        # of every later collection, so no collection ever rescans them; a
+        # collection here instead would cost those 40-50 ms on the first call.
+        gc.freeze()
         _lib = lib
         return lib
 

@@ -334,28 +334,28 @@ def test_skinny_row_blocks_integer_bit_exact(m, dtype):
 
 def test_skinny_rows_take_any_layout_but_a_tiny_b():
     """Above 16 rows the skinny path is the streaming kernel only: A is
-    repacked when its rows are not aligned, B's unaligned rows are
-    register-staged; a B of fewer than 8 elements is a LaunchError for an
-    explicit request, while auto takes the tiled kernel."""
-    from hc import LaunchError
+    repacked when its rows cannot be read in place, B's unaligned rows are
+    read in place by DMA (or register-staged).  A B of fewer than 8 elements
+    is read in place too."""
     from hc.gfx950.workloads import make_inputs
 
     for seed, (m, n, k) in enumerate([(40, 1001, 333), (40, 1000, 333), (17, 9, 7)]):
         a, b = make_inputs("c4_skinny_f16", seed=3 + seed, m=m, n=n, k=k)
         _check(_gemm(a, b, "skinny"), oracle.gemm_c(a, b), k)
     a, b = make_inputs("c4_skinny_f16", seed=9, m=40, n=5, k=1)
-    with pytest.raises(LaunchError, match="B under 8 elements"):
-        _gemm(a, b, "skinny")
-    _check(_gemm(a, b, "auto"), oracle.gemm_c(a, b), 1)
+    _check(_gemm(a, b, "skinny"), oracle.gemm_c(a, b), 1)
+    # (test_paths_for_operands_the_dma_cannot_read covers the LaunchError)
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 8191, 8192), (16, 8191, 8191), (17, 50257, 1024), (64, 1001, 4096),
                                    (128, 333, 2049), (5, 7, 9), (100, 8, 1), (16, 4099, 16384)])
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_streaming_kernel_register_staged_b(m, n, k, dtype):
-    """B's rows not 16-byte aligned (tight, odd N): register-staged B in the
-    streaming kernel, including the chunk that ends at B's last element
-    (loaded as the 16 bytes ending there and shifted), C in a NaN guard band."""
+    """B's rows not 16-byte aligned (tight, odd N): the streaming kernel reads
+    them in place by DMA (16-byte chunks at 2-byte alignment; the chunk
+    holding column N - 1 brings columns that reach no stored element), C in a
+    NaN guard band.  (The page-end test below forces the register-staged
+    form.)"""
     import hc.gfx950 as g
     from hc.gfx950.workloads import make_inputs
 
@@ -371,6 +371,24 @@ def test_streaming_kernel_register_staged_b(m, n, k, dtype):
     mask = np.ones_like(host, dtype=bool)
     mask[1 : m + 1, 1 : n + 1] = False
     assert np.all(np.isnan(host[mask]))
+
+
+@pytest.mark.parametrize("m,n,k,pad", [(16, 8192, 8192, 3), (64, 2048, 4096, 1), (40, 1000, 1024, 5)])
+def test_streaming_kernel_unaligned_a_in_place(m, n, k, pad):
+    """A as a column-sliced view with odd row stride and K a multiple of 8:
+    read in place by the DMA; the row padding holds NaN."""
+    import hc.gfx950 as g
+
+    rng = np.random.default_rng(m + n + k)
+    ai = rng.integers(-4, 5, size=(m, k))
+    bi = rng.integers(-4, 5, size=(k, n))
+    big_a = torch.full((m, k + pad), float("nan"), dtype=torch.float16, device=DEV)
+    big_a[:, :k] = torch.from_numpy(ai).to(DEV, torch.float16)
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device=DEV)
+    print(f"case stream unaligned A in place m={m} n={n} k={k} pad={pad}", flush=True)
+    g.gemm(big_a[:, :k], torch.from_numpy(bi).to(DEV, torch.float16), out=out, algo="skinny")
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), (ai @ bi).astype(np.float32))
 
 
 @pytest.mark.parametrize("m,n,k", [(16, 8192, 8191), (64, 2048, 4095), (128, 1000, 1001), (5, 4096, 2049)])
@@ -691,27 +709,56 @@ def test_unaligned_rows_read_in_place(m, n, k, pad_a, pad_b, algo, dtype):
     assert np.all(np.isnan(host[mask]))
 
 
-def test_unaligned_rows_whose_last_chunk_crosses_a_page_are_repacked():
-    """An A view placed so that its last element ends a 4 KB page: the DMA
-    would read past it into the next page, so the library repacks A instead;
-    the result is the same."""
-    import hc.gfx950 as g
+def test_paths_for_operands_the_dma_cannot_read():
+    """With HCG_UNALIGNED_DMA=0 (a fresh process: the library reads it once)
+    no row that is not 16-byte aligned is read in place, as for an operand
+    whose last chunk would reach past its allocation: the tiled kernel then
+    repacks A and B (C5's shape, +Inf in the row padding), the streaming
+    kernel register-stages B (fp16 and bf16, the chunk ending at B's last
+    element included) and repacks A, and a B of fewer than 8 elements is a
+    LaunchError for an explicit skinny request while auto still runs."""
+    import subprocess
+    import sys
+    import textwrap
 
-    m, n, k = 300, 200, 1027  # K % 8 == 3: the last chunk reads 10 bytes past A's end
-    rng = np.random.default_rng(77)
-    ai = rng.integers(-4, 5, size=(m, k))
-    bi = rng.integers(-4, 5, size=(k, n))
-    buf = torch.zeros(m * k + 8192, dtype=torch.float16, device=DEV)
-    last = buf.data_ptr() + 2 * (m * k - 1)  # last element's address for a view at offset 0
-    off = ((4094 - last % 4096) % 4096) // 2  # move the view so that it ends on a page's last 2 bytes
-    va = buf[off : off + m * k].view(m, k)
-    assert (va.data_ptr() + 2 * (m * k) - 1) % 4096 == 4095
-    va.copy_(torch.from_numpy(ai).to(DEV, torch.float16))
-    vb = torch.from_numpy(bi).to(DEV, torch.float16)
-    print("case page-crossing tail repacked", flush=True)
-    out = g.gemm(va, vb)
-    torch.cuda.synchronize()
-    assert np.array_equal(out.cpu().numpy(), (ai @ bi).astype(np.float32))
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    script = textwrap.dedent(f"""
+        import sys
+        sys.path[:0] = [{os.path.join(root, "5_amd")!r}, {os.path.join(root, "oracle")!r}]
+        import numpy as np, torch
+        import hc.gfx950 as g, hc_oracle as oracle
+        from hc import LaunchError
+        from hc.gfx950.workloads import make_inputs, to_torch
+        dev = torch.device("cuda:0")
+        rng = np.random.default_rng(5)
+        for m, n, k, pad_a, pad_b, algo in [(4095, 3001, 1027, 0, 0, "auto"), (601, 713, 1027, 9, 3, "tiled_256x192"),
+                                            (16, 8191, 4096, 0, 0, "skinny"), (17, 50257, 1024, 0, 0, "skinny"),
+                                            (64, 1001, 4096, 3, 0, "skinny"), (5, 7, 9, 0, 0, "skinny")]:
+            for dt in (torch.float16, torch.bfloat16):
+                ai = rng.integers(-4, 5, size=(m, k)); bi = rng.integers(-4, 5, size=(k, n))
+                big_a = torch.full((m, k + pad_a), float("inf"), dtype=dt, device=dev)
+                big_b = torch.full((k, n + pad_b), float("inf"), dtype=dt, device=dev)
+                big_a[:, :k] = torch.from_numpy(ai).to(dev, dt); big_b[:, :n] = torch.from_numpy(bi).to(dev, dt)
+                out = g.gemm(big_a[:, :k], big_b[:, :n], algo=algo)
+                torch.cuda.synchronize()
+                ok = np.array_equal(out.cpu().numpy(), (ai @ bi).astype(np.float32))
+                print(m, n, k, algo, dt, ok, flush=True)
+                assert ok
+        a, b = make_inputs("c4_skinny_f16", seed=9, m=40, n=5, k=1)
+        ta, tb = to_torch(a, "float16", dev), to_torch(b, "float16", dev)
+        try:
+            g.gemm(ta, tb, algo="skinny")
+            raise SystemExit("expected a LaunchError for a B of 5 elements")
+        except LaunchError as exc:
+            assert "B under 8 elements" in str(exc), exc
+        out = g.gemm(ta, tb, algo="auto")
+        torch.cuda.synchronize()
+        assert oracle.parity_check(out.cpu().numpy(), oracle.gemm_c(a, b), 1).ok
+    """)
+    print("case HCG_UNALIGNED_DMA=0 repack and register-staged paths", flush=True)
+    env = dict(os.environ, HCG_UNALIGNED_DMA="0")
+    proc = subprocess.run([sys.executable, "-c", script], env=env, capture_output=True, text=True, timeout=110)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
 
 
 @pytest.mark.parametrize("algo", ["auto"] + TILE_ALGOS)

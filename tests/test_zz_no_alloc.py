@@ -105,18 +105,10 @@ def test_noalloc_matches_hcg_gemm_on_two_calls(first, second, kind):
 
 def test_noalloc_rejects_a_call_beyond_its_scratch_before_any_launch():
     native, lib = _lib()
-    # A with unaligned rows placed so that its last element ends a 4 KB page:
-    # the DMA cannot read its last chunk in place (it would reach the next
-    # page), so A needs a repacked copy, 8192 x 4104 x 2 bytes (64 MiB), more
-    # than the 32 MiB array.
-    m, n, k = 8192, 512, 4097
-    rng = np.random.default_rng(5)
-    buf = torch.zeros(m * k + 8192, dtype=torch.float16, device=DEV)
-    last = buf.data_ptr() + 2 * (m * k - 1)
-    off = ((4094 - last % 4096) % 4096) // 2
-    ta = buf[off : off + m * k].view(m, k)
-    ta.copy_(torch.from_numpy(rng.integers(-4, 5, size=(m, k)).astype(np.float16)).to(DEV))
-    tb = torch.from_numpy(rng.integers(-4, 5, size=(k, n)).astype(np.float16)).to(DEV)
+    # 40 rows (the streaming kernel) with K not a multiple of 8: A is
+    # repacked, 40 x 524296 x 2 bytes (42 MB), more than the 32 MiB array.
+    m, n, k = 40, 128, (1 << 19) + 1
+    _, _, ta, tb = _operands(m, n, k, k, n, "int", seed=5)
     print("case noalloc over the scratch limit", flush=True)
     rc, got, band = _call("hcg_gemm_noalloc", ta, k, tb, n, m, n, k)
     assert rc == native.HCG_EINVAL
