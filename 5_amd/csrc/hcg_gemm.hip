@@ -2490,15 +2490,21 @@ int run_skinny(const Scratch& sc, int dtype, const void* A, int64_t lda, const v
 
 // The narrow-N streaming kernel: N <= 64, A by DMA or through registers,
 // byte offsets below 2^31.
-// B's rows need not be aligned: B (at most 32 columns) is repacked when they
-// are not.  A goes by DMA when its rows are 16-byte aligned, K is a multiple
-// of 8 and its offsets stay below 2^31, and through registers otherwise.
+// B's rows need not be aligned: B (at most 64 columns) is read in place by
+// the DMA when its last chunk is safely readable (chunk_tail_readable; the
+// chunk holding column N - 1 brings columns that reach only C columns >= N)
+// and repacked otherwise.  A goes by DMA when K is a multiple of 8 (no chunk
+// straddles K), its rows are 16-byte aligned or its last chunk is safely
+// readable, and its offsets stay below 2^31; through registers otherwise.
 bool rowstream_a_dma(const void* A, int64_t lda, int64_t M, int64_t K) {
-  return aligned16(A) && lda % 8 == 0 && K % 8 == 0 &&
-         ((int64_t)round_up(M, kRsRows) * lda + round_up(K, kRsStep)) * 2 < ((int64_t)1 << 31);
+  return K % 8 == 0 && ((int64_t)round_up(M, kRsRows) * lda + round_up(K, kRsStep)) * 2 < ((int64_t)1 << 31) &&
+         ((aligned16(A) && lda % 8 == 0) || (aligned2(A) && chunk_tail_readable(A, M, K, lda)));
+}
+bool rowstream_b_in_place(const void* B, int64_t ldb, int64_t N, int64_t K) {
+  return (aligned16(B) && ldb % 8 == 0) || (aligned2(B) && chunk_tail_readable(B, K, N, ldb));
 }
 bool rowstream_fits(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K) {
-  const int64_t ldb_use = aligned16(B) && ldb % 8 == 0 ? ldb : round_up(N, 8);
+  const int64_t ldb_use = rowstream_b_in_place(B, ldb, N, K) ? ldb : round_up(N, 8);
   return N <= 64 && lda < ((int64_t)1 << 31) &&
          ((int64_t)round_up(K, kRsStep) * ldb_use + 64) * 2 < ((int64_t)1 << 31);
 }
@@ -2550,9 +2556,9 @@ int run_rowstream(const Scratch& sc, int dtype, const void* A, int64_t lda, cons
   if (splits > max_by_k) splits = max_by_k;
   if (splits > kStMaxSplitsLoop) splits = kStMaxSplitsLoop;
   if (splits < 1) splits = 1;
-  // Workspace: B repacked to zero-padded 16-byte aligned rows (when its rows
-  // are not), then the split partials [splits][M][N].
-  const bool b_ok = aligned16(B) && ldb % 8 == 0;
+  // Workspace: B repacked to zero-padded 16-byte aligned rows (when the DMA
+  // cannot read it in place), then the split partials [splits][M][N].
+  const bool b_ok = rowstream_b_in_place(B, ldb, N, K);
   const int64_t ldb_use = b_ok ? ldb : round_up(N, 8);
   const size_t b_sz = b_ok ? 0 : round_up((size_t)K * ldb_use * 2, 256);
   splits = fit_splits(splits, (size_t)M * N * sizeof(float), sc.room(b_sz));
@@ -2576,8 +2582,9 @@ int run_rowstream(const Scratch& sc, int dtype, const void* A, int64_t lda, cons
     }
     if (a.splits > 1) a.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + b_sz);
   }
-  a.a_bytes = a_dma ? (int)round_up((size_t)(((int64_t)M - 1) * lda + K) * 2, 16) : 0;
-  a.b_bytes = (int)round_up((size_t)(((int64_t)K - 1) * a.ldb + N) * 2, 16);
+  // Extents end with the chunk that holds the last element.
+  a.a_bytes = a_dma ? (int)((((int64_t)M - 1) * lda + (int64_t)round_up(K, 8)) * 2) : 0;
+  a.b_bytes = (int)((((int64_t)K - 1) * a.ldb + (int64_t)round_up(N, 8)) * 2);
   const dim3 grid((unsigned)(nrb * a.splits));
   const int nb = N <= 16 ? 16 : N <= 32 ? 32 : 64;
   if (dtype == HCG_F16) {

@@ -373,6 +373,31 @@ def test_streaming_kernel_register_staged_b(m, n, k, dtype):
     assert np.all(np.isnan(host[mask]))
 
 
+@pytest.mark.parametrize("m,n,k,pad_a,pad_b", [(4096, 13, 4096, 3, 0), (3000, 40, 2048, 0, 5), (777, 64, 1024, 1, 1)])
+def test_narrow_kernel_unaligned_rows_in_place(m, n, k, pad_a, pad_b):
+    """The narrow kernel reads A (K a multiple of 8) and B with rows that are
+    not 16-byte aligned in place; row padding holds NaN."""
+    import hc.gfx950 as g
+
+    rng = np.random.default_rng(m + n + k)
+    ai = rng.integers(-4, 5, size=(m, k))
+    bi = rng.integers(-4, 5, size=(k, n))
+    big_a = torch.full((m, k + pad_a), float("nan"), dtype=torch.float16, device=DEV)
+    big_b = torch.full((k, n + pad_b), float("nan"), dtype=torch.float16, device=DEV)
+    big_a[:, :k] = torch.from_numpy(ai).to(DEV, torch.float16)
+    big_b[:, :n] = torch.from_numpy(bi).to(DEV, torch.float16)
+    guard = torch.full((m + 2, n + 2), float("nan"), dtype=torch.float32, device=DEV)
+    out = guard[1 : m + 1, 1 : n + 1]
+    print(f"case narrow unaligned in place m={m} n={n} k={k} pad_a={pad_a} pad_b={pad_b}", flush=True)
+    g.gemm(big_a[:, :k], big_b[:, :n], out=out, algo="narrow")
+    torch.cuda.synchronize()
+    host = guard.cpu().numpy()
+    assert np.array_equal(host[1 : m + 1, 1 : n + 1], (ai @ bi).astype(np.float32))
+    mask = np.ones_like(host, dtype=bool)
+    mask[1 : m + 1, 1 : n + 1] = False
+    assert np.all(np.isnan(host[mask]))
+
+
 @pytest.mark.parametrize("m,n,k,pad", [(16, 8192, 8192, 3), (64, 2048, 4096, 1), (40, 1000, 1024, 5)])
 def test_streaming_kernel_unaligned_a_in_place(m, n, k, pad):
     """A as a column-sliced view with odd row stride and K a multiple of 8:
@@ -715,8 +740,9 @@ def test_paths_for_operands_the_dma_cannot_read():
     whose last chunk would reach past its allocation: the tiled kernel then
     repacks A and B (C5's shape, +Inf in the row padding), the streaming
     kernel register-stages B (fp16 and bf16, the chunk ending at B's last
-    element included) and repacks A, and a B of fewer than 8 elements is a
-    LaunchError for an explicit skinny request while auto still runs."""
+    element included) and repacks A, the narrow kernel repacks B and stages
+    A through registers, and a B of fewer than 8 elements is a LaunchError
+    for an explicit skinny request while auto still runs."""
     import subprocess
     import sys
     import textwrap
@@ -733,7 +759,8 @@ def test_paths_for_operands_the_dma_cannot_read():
         rng = np.random.default_rng(5)
         for m, n, k, pad_a, pad_b, algo in [(4095, 3001, 1027, 0, 0, "auto"), (601, 713, 1027, 9, 3, "tiled_256x192"),
                                             (16, 8191, 4096, 0, 0, "skinny"), (17, 50257, 1024, 0, 0, "skinny"),
-                                            (64, 1001, 4096, 3, 0, "skinny"), (5, 7, 9, 0, 0, "skinny")]:
+                                            (64, 1001, 4096, 3, 0, "skinny"), (5, 7, 9, 0, 0, "skinny"),
+                                            (3000, 13, 4096, 0, 0, "narrow"), (300, 40, 1024, 3, 5, "narrow")]:
             for dt in (torch.float16, torch.bfloat16):
                 ai = rng.integers(-4, 5, size=(m, k)); bi = rng.integers(-4, 5, size=(k, n))
                 big_a = torch.full((m, k + pad_a), float("inf"), dtype=dt, device=dev)
