@@ -371,6 +371,33 @@ __shared__ __attribute__((aligned(1024))) unsigned char g_t128_s0[dma_stage_byte
 __shared__ __attribute__((aligned(1024))) unsigned char g_t128_s1[dma_stage_bytes<128>()];
 __shared__ __attribute__((aligned(1024))) unsigned char g_t128_s2[dma_stage_bytes<128>()];
 
+// A2 layout (TM = 256, 4 stages): A moves in 64-wide K pairs of tiles, one
+// 128-byte piece per row, into two 32 KB double stages; B keeps four 16 KB
+// stages.  Separate objects, so that no DMA shares an object with reads in
+// flight.
+__shared__ __attribute__((aligned(1024))) unsigned char g_a2_d0[256 * 64 * 2];
+__shared__ __attribute__((aligned(1024))) unsigned char g_a2_d1[256 * 64 * 2];
+__shared__ __attribute__((aligned(1024))) unsigned char g_b2_s0[kDmaK * kTileN * 2];
+__shared__ __attribute__((aligned(1024))) unsigned char g_b2_s1[kDmaK * kTileN * 2];
+__shared__ __attribute__((aligned(1024))) unsigned char g_b2_s2[kDmaK * kTileN * 2];
+__shared__ __attribute__((aligned(1024))) unsigned char g_b2_s3[kDmaK * kTileN * 2];
+template <int D>
+__device__ __forceinline__ unsigned char* a2_dstage() {
+  if constexpr (D == 0) return g_a2_d0;
+  else return g_a2_d1;
+}
+template <int S>
+__device__ __forceinline__ unsigned char* b2_stage() {
+  if constexpr (S == 0) return g_b2_s0;
+  else if constexpr (S == 1) return g_b2_s1;
+  else if constexpr (S == 2) return g_b2_s2;
+  else return g_b2_s3;
+}
+// Physical 16-byte chunk of logical chunk c (of 8) in an A2 row: rows two
+// apart take different chunks, so a 16-lane group of ds_read_b128 (16
+// consecutive rows of 128 bytes) covers all 64 banks once.
+__device__ __forceinline__ int a2_chunk_swz(int row, int c) { return c ^ ((row >> 1) & 7); }
+
 template <int TM, int S>
 __device__ __forceinline__ unsigned char* dma_stage() {
   if constexpr (TM == 256) {
@@ -419,9 +446,19 @@ __device__ __forceinline__ int b_chunk_swz(int k, int c) {
 // operands with unaligned rows are read in place; the host checks that the
 // bytes a last chunk reads past an operand's end stay in the page of its
 // last element.)
-template <int DT, int TM, int TN, int STAGES, bool WIDE = false, bool KT = false>
+//
+// A2 (TM = 256, 4 stages, not WIDE): A moves HBM -> LDS for two K tiles at
+// a time, one 128-byte piece of each row per DMA lane group, instead of a
+// 64-byte piece per tile: half the L2 requests for A, and never two lines
+// for one tile's piece when rows are not 128-byte aligned.  Per-workgroup
+// timestamps showed those requests, not MFMA issue, setting the K loop's
+// pace at K ~ 1K (4096 x 3008 x 1024: 28.7k shader cycles at lda = 1024
+// against 38.2k at lda = 1032; with A's requests collapsed, 27.5k for both).
+template <int DT, int TM, int TN, int STAGES, bool WIDE = false, bool KT = false, bool A2 = false>
 __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_kernel(FastArgs g) {
   static_assert((TM == 256 && STAGES == 4) || (TM == 128 && STAGES == 3), "tile variant");
+  static_assert(!A2 || (TM == 256 && STAGES == 4 && !WIDE), "A2 form");
+  constexpr int kADma2 = TM / 32;  // A2: A DMA instructions per wave per pair of K tiles
   static_assert(TN == 256 || TN == 192 || TN == 128 || TN == 64, "tile width");
   constexpr int kMi = TM / 64;            // 32-row MFMA tiles per wave
   constexpr int kNi = TN / 64;            // 32-column MFMA tiles per wave
@@ -487,6 +524,21 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
     if constexpr (KT && !WIDE)
       if (m0 + row >= g.M) a_off[i] = g.a_bytes;
   }
+  // A2 roles: wave w fills rows 64w .. 64w + 63 of a double stage, 8 rows
+  // (1 KB) per instruction; lane l covers row 64w + 8i + l/8 at physical
+  // chunk l%8 (logical chunk a2_chunk_swz of it) of the 64-wide K pair.
+  int a2_off[A2 ? kADma2 : 1], a2_col[A2 ? kADma2 : 1];
+  if constexpr (A2) {
+#pragma unroll
+    for (int i = 0; i < kADma2; ++i) {
+      const int row = 64 * wave + 8 * i + (lane >> 3);
+      const int c = a2_chunk_swz(row, lane & 7);
+      a2_col[i] = c * 8;
+      a2_off[i] = ((m0 + row) * g.lda + c * 8) * 2;
+      if constexpr (KT)
+        if (m0 + row >= g.M) a2_off[i] = g.a_bytes;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int blk = wave * 4 + i;
@@ -524,8 +576,25 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
         dma16(rsrc_a, dst, dma_offset(k0 + a_col[i] < g.K, a_off[i] + k0 * 2));
     }
   };
+  // A2: the A parts of K tiles kt and kt + 1 (kt even) into double stage D.
+  auto issue_a2 = [&](auto dc, auto full, int kt) {
+    unsigned char* st = a2_dstage<decltype(dc)::value>();
+    const int k0 = kt * kDmaK;
+#pragma unroll
+    for (int i = 0; i < kADma2; ++i) {
+      lds_void* dst = (lds_void*)(st + (wave * kADma2 + i) * 1024);
+      if constexpr (decltype(full)::value)
+        dma16(rsrc_a, dst, a2_off[i], k0 * 2);
+      else
+        dma16(rsrc_a, dst, dma_offset(k0 + a2_col[i] < g.K, a2_off[i] + k0 * 2));
+    }
+  };
   auto issue_b = [&](auto sc, auto full, int kt) {
-    unsigned char* st = dma_stage<TM, decltype(sc)::value>();
+    unsigned char* bst;  // the stage's B part
+    if constexpr (A2)
+      bst = b2_stage<decltype(sc)::value>();
+    else
+      bst = dma_stage<TM, decltype(sc)::value>() + kABytes;
     const int k0 = kt * kDmaK;
     if constexpr (WIDE) {
       // Resource for rows k0 .. k0 + 31 from column n0; rows past K are past
@@ -535,11 +604,11 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
       const __amdgpu_buffer_rsrc_t rk = make_rsrc(
           g.B + (int64_t)k0 * g.ldb + n0, rows > 0 ? ((rows - 1) * g.ldb + ((g.N - n0 + 7) & ~7)) * 2 : 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dma16(rk, (lds_void*)(st + kABytes + (wave * 4 + i) * 1024), b_off[i]);
+      for (int i = 0; i < 4; ++i) dma16(rk, (lds_void*)(bst + (wave * 4 + i) * 1024), b_off[i]);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        lds_void* dst = (lds_void*)(st + kABytes + (wave * 4 + i) * 1024);
+        lds_void* dst = (lds_void*)(bst + (wave * 4 + i) * 1024);
         if constexpr (decltype(full)::value)
           dma16(rsrc_b, dst, b_off[i], k0 * g.ldb * 2);
         else
@@ -556,7 +625,9 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
     for (int mi = 0; mi < kMi; ++mi) {
       const int row = wm * (TM / 2) + mi * 32 + (lane & 31);
       const int c = kk * 2 + (lane >> 5);
-      fa_addr[kk][mi] = row * 64 + a_chunk_swz(row, c) * 16;
+      // A2: the first tile of the pair; the second's chunk is c + 4, which
+      // flips bit 2 of the physical chunk (address bit 6).
+      fa_addr[kk][mi] = A2 ? row * 128 + a2_chunk_swz(row, c) * 16 : row * 64 + a_chunk_swz(row, c) * 16;
     }
 #pragma unroll
     for (int ni = 0; ni < kNi; ++ni) {
@@ -565,21 +636,30 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
         const int sl = lane & 15, grp = lane >> 4;
         const int krow = kk * 16 + 8 * (grp >> 1) + 4 * h + (sl >> 2);
         const int ncol = wn * (TN / 2) + ni * 32 + 16 * (grp & 1) + 4 * (sl & 3);
-        fb_addr[kk][ni][h] = kABytes + krow * 512 + b_chunk_swz(krow, ncol >> 3) * 16 + (ncol & 7) * 2;
+        fb_addr[kk][ni][h] = (A2 ? 0 : kABytes) + krow * 512 + b_chunk_swz(krow, ncol >> 3) * 16 + (ncol & 7) * 2;
       }
     }
   }
 
   auto read_frags = [&](auto sc, int kk, u32x4 (&fa)[kMi], u32x4 (&fb)[kNi]) {
-    const unsigned char* st = dma_stage<TM, decltype(sc)::value>();
+    constexpr int S = decltype(sc)::value;
+    const unsigned char* ast;
+    const unsigned char* bst;
+    if constexpr (A2) {
+      ast = a2_dstage<(S >> 1) & 1>();
+      bst = b2_stage<S>();
+    } else {
+      ast = bst = dma_stage<TM, S>();
+    }
+    constexpr int kHalf = (A2 && (S & 1)) ? 64 : 0;  // A2: second tile of the pair
 #pragma unroll
-    for (int mi = 0; mi < kMi; ++mi) fa[mi] = *reinterpret_cast<const u32x4*>(st + fa_addr[kk][mi]);
+    for (int mi = 0; mi < kMi; ++mi) fa[mi] = *reinterpret_cast<const u32x4*>(ast + (fa_addr[kk][mi] ^ kHalf));
 #pragma unroll
     for (int ni = 0; ni < kNi; ++ni) {
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(st + fb_addr[kk][ni][0]));
+          (__attribute__((address_space(3))) s16x4*)(bst + fb_addr[kk][ni][0]));
       const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(st + fb_addr[kk][ni][1]));
+          (__attribute__((address_space(3))) s16x4*)(bst + fb_addr[kk][ni][1]));
       const uint64_t l64 = __builtin_bit_cast(uint64_t, lo), h64 = __builtin_bit_cast(uint64_t, hi);
       fb[ni] = u32x4{(uint32_t)l64, (uint32_t)(l64 >> 32), (uint32_t)h64, (uint32_t)(h64 >> 32)};
     }
@@ -629,8 +709,10 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
       __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
       if (2 * m < kReads) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
       int loads = 0;
+      if constexpr (nv > 0) {
 #pragma unroll
-      for (int v = 0; v < nv; ++v) loads += (v * kMfmas / nv + shift == m) ? 1 : 0;
+        for (int v = 0; v < nv; ++v) loads += (v * kMfmas / nv + shift == m) ? 1 : 0;
+      }
       if (loads == 1) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 1, 0);
       if (loads == 2) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 2, 0);
     }
@@ -655,31 +737,55 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
     schedule(std::integral_constant<int, 4>{});
     // Tile kt+1 has landed for this wave (the two tiles requested after it
     // may still be in flight); this wave's fragment reads of tile kt are
-    // complete.
-    wait_vmcnt<(STAGES - 2) * kDmaPerWave>();
+    // complete.  A2: after tile kt+1's last load this wave issued the B
+    // parts of kt+2 and kt+3, and for even kt also the A pair (kt+2, kt+3).
+    if constexpr (A2)
+      wait_vmcnt<(S & 1) ? 8 : 8 + kADma2>();
+    else
+      wait_vmcnt<(STAGES - 2) * kDmaPerWave>();
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    // Every wave is past its reads of tile kt: stage S takes tile kt+STAGES.
+    // Every wave is past its reads of tile kt: stage S takes tile kt+STAGES
+    // (A2: after odd kt, the A double stage of kt-1 and kt takes the pair
+    // kt+3, kt+4).
     read_frags(StageC<(S + 1) % STAGES>{}, 0, fa0, fb0);
     if constexpr (kMask) mask_tail(fa0, kt + 1, 0);
-    issue_a(sc, full, kt + STAGES);
-    mfma_block(fa1, fb1);
-    schedule(std::integral_constant<int, kADma>{});
+    if constexpr (!A2) {
+      issue_a(sc, full, kt + STAGES);
+      mfma_block(fa1, fb1);
+      schedule(std::integral_constant<int, kADma>{});
+    } else if constexpr (S & 1) {
+      issue_a2(std::integral_constant<int, (S >> 1) & 1>{}, full, kt + 3);
+      mfma_block(fa1, fb1);
+      schedule(std::integral_constant<int, kADma2>{});
+    } else {
+      mfma_block(fa1, fb1);
+      schedule(std::integral_constant<int, 0>{});
+    }
   };
 
-  // Prologue: tiles 0..STAGES-2 and the A part of tile STAGES-1 in flight;
-  // wait for tile 0.
-  issue_a(StageC<0>{}, std::false_type{}, 0);
-  issue_b(StageC<0>{}, std::false_type{}, 0);
-  issue_a(StageC<1>{}, std::false_type{}, 1);
-  issue_b(StageC<1>{}, std::false_type{}, 1);
-  if constexpr (STAGES == 4) {
-    issue_a(StageC<2>{}, std::false_type{}, 2);
+  // Prologue: tiles 0..STAGES-2 and the A part of tile STAGES-1 in flight
+  // (A2: A pairs (0, 1) and (2, 3), B of tiles 0..2); wait for tile 0.
+  if constexpr (A2) {
+    issue_a2(std::integral_constant<int, 0>{}, std::false_type{}, 0);
+    issue_b(StageC<0>{}, std::false_type{}, 0);
+    issue_b(StageC<1>{}, std::false_type{}, 1);
     issue_b(StageC<2>{}, std::false_type{}, 2);
+    issue_a2(std::integral_constant<int, 1>{}, std::false_type{}, 2);
+    wait_vmcnt<8 + kADma2>();
+  } else {
+    issue_a(StageC<0>{}, std::false_type{}, 0);
+    issue_b(StageC<0>{}, std::false_type{}, 0);
+    issue_a(StageC<1>{}, std::false_type{}, 1);
+    issue_b(StageC<1>{}, std::false_type{}, 1);
+    if constexpr (STAGES == 4) {
+      issue_a(StageC<2>{}, std::false_type{}, 2);
+      issue_b(StageC<2>{}, std::false_type{}, 2);
+    }
+    issue_a(StageC<STAGES - 1>{}, std::false_type{}, STAGES - 1);
+    wait_vmcnt<(STAGES - 2) * kDmaPerWave + kADma>();
   }
-  issue_a(StageC<STAGES - 1>{}, std::false_type{}, STAGES - 1);
-  wait_vmcnt<(STAGES - 2) * kDmaPerWave + kADma>();
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   read_frags(StageC<0>{}, 0, fa0, fb0);
@@ -720,8 +826,12 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
   // disjoint banks.
   __builtin_amdgcn_s_barrier();  // every wave is done reading the stages
   constexpr int kEpRow = 136;     // floats per staged row
-  float* ep = reinterpret_cast<float*>((wave < 2 ? dma_stage<TM, 0>() : dma_stage<TM, 1>()) +
-                                       (wave & 1) * (16 * kEpRow * 4));
+  unsigned char* ep_base;
+  if constexpr (A2)
+    ep_base = wave < 2 ? a2_dstage<0>() : a2_dstage<1>();
+  else
+    ep_base = wave < 2 ? dma_stage<TM, 0>() : dma_stage<TM, 1>();
+  float* ep = reinterpret_cast<float*>(ep_base + (wave & 1) * (16 * kEpRow * 4));
   const bool full = g.c_vec && (m0 + TM <= g.M) && (n0 + TN <= g.N);
   const int col_l = lane & 31;
   const int row_l = (lane >> 5) * 4;
@@ -2253,12 +2363,15 @@ template <int DT, bool WIDE, bool KT = false>
 int launch_dma(const FastArgs& a, int shape, hipStream_t stream) {
   const dim3 grid((unsigned)(a.tiles_m * a.tiles_n * (a.splits > 1 ? a.splits : 1)));
   const dim3 block(kTiledThreads);
+  // 256-row tiles move A as 64-wide K pairs (A2) unless the operands need
+  // the WIDE form.
+  constexpr bool kA2 = !WIDE;
   switch (shape) {
-    case 0: gemm_dma_kernel<DT, 256, 256, 4, WIDE, KT><<<grid, block, 0, stream>>>(a); break;
-    case 1: gemm_dma_kernel<DT, 256, 192, 4, WIDE, KT><<<grid, block, 0, stream>>>(a); break;
+    case 0: gemm_dma_kernel<DT, 256, 256, 4, WIDE, KT, kA2><<<grid, block, 0, stream>>>(a); break;
+    case 1: gemm_dma_kernel<DT, 256, 192, 4, WIDE, KT, kA2><<<grid, block, 0, stream>>>(a); break;
     case 2: gemm_dma_kernel<DT, 128, 256, 3, WIDE, KT><<<grid, block, 0, stream>>>(a); break;
     case 3: gemm_dma_kernel<DT, 128, 128, 3, WIDE, KT><<<grid, block, 0, stream>>>(a); break;
-    default: gemm_dma_kernel<DT, 256, 64, 4, WIDE, KT><<<grid, block, 0, stream>>>(a); break;
+    default: gemm_dma_kernel<DT, 256, 64, 4, WIDE, KT, kA2><<<grid, block, 0, stream>>>(a); break;
   }
   HCG_HIP_CHECK(hipGetLastError());
   return HCG_OK;
