@@ -99,9 +99,13 @@ __global__ __launch_bounds__(256) void probe_mfma_kernel(int iters, float* sink,
   for (int j = 0; j < 8; ++j) acc[j] = f32x16{};
   const uint64_t t0 = __builtin_amdgcn_s_memtime();
   const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
-  for (int i = 0; i < iters; ++i) {
+  // Four rounds (32 MFMAs) per trip, so the loop's branch (several cycles
+  // per taken branch) costs little; iters is a multiple of 4.
+  for (int i = 0; i < iters; i += 4) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = mfma<DT>(fa[j & 3], fb[(j + (j >> 2)) & 3], acc[j]);
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = mfma<DT>(fa[j & 3], fb[(j + (j >> 2)) & 3], acc[j]);
   }
   const uint64_t t1 = __builtin_amdgcn_s_memtime();
   const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
@@ -165,7 +169,8 @@ extern "C" {
 
 int hcg_probe_mfma(int dtype, int iters, int blocks, float* sink, uint64_t* clocks, void* stream) {
   if (dtype != 0 && dtype != 1) return probe_error(1, "dtype must be 0 (fp16) or 1 (bf16), got %d", dtype);
-  if (iters <= 0 || blocks <= 0) return probe_error(1, "iters and blocks must be positive");
+  if (iters <= 0 || blocks <= 0 || iters % 4 != 0)
+    return probe_error(1, "iters must be a positive multiple of 4 and blocks positive");
   if (!sink || !clocks) return probe_error(1, "sink or clocks is NULL");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == 0)

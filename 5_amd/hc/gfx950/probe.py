@@ -81,7 +81,8 @@ def mfma(torch: Any, stream: Any, dtype: int = 0, warm_s: float = 0.3, launches:
     """Pure MFMA issue on every CU (`per_cu` 4-wave workgroups per CU, 8
     independent 32x32x16 chains per wave): TFLOP/s, the fraction of the
     CUs' issue rate at the measured mean clock (the launch lasts as long as
-    the slowest XCD's clock allows, so this stays below 1), and the shader
+    the slowest XCD's clock allows, so this stays below 1), shader cycles
+    per MFMA inside the loop (32 at the full issue rate), and the shader
     clock (cycles over 100 MHz real-time ticks, per workgroup)."""
     lib = load()
     dev = torch.cuda.current_device()
@@ -103,6 +104,7 @@ def mfma(torch: Any, stream: Any, dtype: int = 0, warm_s: float = 0.3, launches:
     # per 32 clocks each)
     issue = tflops * 1e12 / (cus * 4096 * float(mhz.mean()) * 1e6)
     return {"dtype": "f16" if dtype == 0 else "bf16", "tflops": tflops, "issue_frac": issue,
+            "cycles_per_mfma": float(c[:, 0].mean()) / (iters * 8),
             "us_per_launch": seconds * 1e6, "clock_mhz": float(mhz.mean()),
             "clock_mhz_min": float(mhz.min()), "clock_mhz_max": float(mhz.max()),
             "shape": f"{blocks} workgroups x 4 waves x 8 chains x {iters} rounds of v_mfma_f32_32x32x16"}

@@ -26,7 +26,7 @@ extern "C" {
 #endif
 
 /* `blocks` workgroups of 256 threads (4 waves); each wave issues `iters`
- * rounds of 8 independent 32x32x16 MFMAs (dtype 0 fp16, 1 bf16) on
+ * (a multiple of 4) rounds of 8 independent 32x32x16 MFMAs (dtype 0 fp16, 1 bf16) on
  * pseudo-random operands in [-1, 1) -- 2 * 32 * 32 * 16 * 8 * iters flops
  * per wave.  `sink` (blocks * 256 floats) receives the accumulators' sums;
  * `clocks` (2 * blocks uint64) receives, per workgroup, the shader-clock

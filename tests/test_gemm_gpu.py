@@ -915,6 +915,46 @@ def test_random_shapes_and_layouts_against_oracle(i):
     assert np.all(np.isnan(host[mask]))
 
 
+# Views that start 1..7 elements into their allocation (so rows sit at any
+# 2-byte alignment) with odd row pitches, for every kernel choice: the DMA
+# kernels read such rows in place, and a chunk past a row's end must never
+# reach C.  NaN fills everything outside the views.
+_OFFSET_ALGOS = ["auto", "auto", "tiled", "tiled_256x256", "tiled_256x192", "tiled_128x256", "tiled_128x128",
+                 "tiled_256x64", "skinny", "narrow", "generic"]
+
+
+@pytest.mark.parametrize("i", range(44))
+def test_random_base_offsets_against_oracle(i):
+    import hc.gfx950 as g
+    from hc.gfx950.workloads import make_inputs
+
+    rng = np.random.default_rng(70000 + i)
+    algo = _OFFSET_ALGOS[i % len(_OFFSET_ALGOS)]
+    m = int(rng.integers(1, 129)) if algo == "skinny" or rng.random() < 0.2 else int(rng.integers(1, 1300))
+    n = int(rng.integers(1, 65)) if algo == "narrow" else int(rng.integers(1, 1300))
+    k = int(rng.choice([rng.integers(1, 64), rng.integers(64, 3000)]))
+    pad_a, pad_b = int(rng.choice([0, 1, 2, 3, 7, 64])), int(rng.choice([0, 1, 2, 5, 64]))
+    off_a, off_b = int(rng.integers(0, 8)), int(rng.integers(0, 8))
+    dtype = "float16" if rng.random() < 0.7 else "bfloat16"
+    print(f"case offsets {i}: {algo} {dtype} m={m} n={n} k={k} pads={pad_a},{pad_b} offs={off_a},{off_b}",
+          flush=True)
+    a, b = make_inputs("c2_4096_f16" if dtype == "float16" else "c3_8192_bf16", seed=i, m=m, n=n, k=k)
+    tdt = torch.float16 if dtype == "float16" else torch.bfloat16
+    big_a = torch.full((m, off_a + k + pad_a), float("nan"), dtype=tdt, device=DEV)
+    big_b = torch.full((k, off_b + n + pad_b), float("nan"), dtype=tdt, device=DEV)
+    va, vb = big_a[:, off_a : off_a + k], big_b[:, off_b : off_b + n]
+    va.copy_(_dev(a, dtype))
+    vb.copy_(_dev(b, dtype))
+    guard = torch.full((m + 1, n + 2), float("nan"), dtype=torch.float32, device=DEV)
+    g.gemm(va, vb, out=guard[:m, 1 : n + 1], algo=algo)
+    torch.cuda.synchronize()
+    host = guard.cpu().numpy()
+    _check(host[:m, 1 : n + 1], oracle.gemm_c(a, b, oracle.F16 if dtype == "float16" else oracle.BF16), k)
+    mask = np.ones_like(host, dtype=bool)
+    mask[:m, 1 : n + 1] = False
+    assert np.all(np.isnan(host[mask]))
+
+
 # Extreme aspect ratios: K in the millions for a 1 x 1 or 3 x 5 output,
 # one-column and one-row outputs of 10^5, K of 1..9, through every kernel
 # that takes the shape, C in a NaN guard band.
