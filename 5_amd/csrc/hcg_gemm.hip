@@ -2963,12 +2963,15 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
   // HBM-bound: B is streamed once through a skinny kernel instead of
   // occupying only N/128 workgroups of the tiled kernel.  Rows 65..128 (the
   // streaming kernel's eight row blocks) go to the tiled kernel, which splits
-  // K to fill the chip, when B's rows are aligned (no repack of B): fp16 us,
-  // streaming -> tiled: 128^3 5.9 -> 4.4, 128 x 512 x 512 9.2 -> 6.4,
-  // 128 x 2048 x 2048 14.1 -> 11.1, 128 x 8192 x 1024 16.2 -> 9.8,
-  // 128 x 16384 x 512 17.2 -> 7.3, 128 x 8192 x 8192 38.3 -> 35.7; the
-  // streaming kernel led by at most 8% (80 x 4096 x 4096 16.6 against 18.0).
-  const bool tiled_rows = M > 64 && aligned16(B) && ldb % 8 == 0;
+  // K to fill the chip, when it reads B in place: fp16 us, streaming ->
+  // tiled: 128^3 5.9 -> 4.4, 128 x 512 x 512 9.2 -> 6.4, 128 x 2048 x 2048
+  // 14.1 -> 11.1, 128 x 8192 x 1024 16.2 -> 9.8, 128 x 16384 x 512 17.2 ->
+  // 7.3, 128 x 8192 x 8192 38.3 -> 35.7; with B's rows unaligned 128 x 3001
+  // x 1027 16.4 -> 14.0, 100 x 50257 x 1024 35.4 -> 23.6, 72 x 12289 x 4096
+  // 34.1 -> 27.8.  The streaming kernel led by at most 9% (80 x 4096 x 4096
+  // 16.6 against 18.0, 128 x 1001 x 2048 12.1 / 13.2).
+  const bool tiled_rows = M > 64 && ((aligned16(B) && ldb % 8 == 0) ||
+                                     (K > 0 && N > 0 && aligned2(B) && chunk_tail_readable(B, K, N, ldb)));
   const bool use_skinny =
       !use_narrow && (algo == HCG_ALGO_SKINNY ||
                       (algo == HCG_ALGO_AUTO && (M <= 16 || (!tiled_rows && stream_fits(A, lda, B, ldb, M, N, K)))));
