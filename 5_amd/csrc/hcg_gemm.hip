@@ -1831,11 +1831,24 @@ __global__ __launch_bounds__(NB == 64 ? 512 : 256) void gemm_rowstream_kernel(Ro
 #pragma unroll
   for (int cb = 0; cb < kBlocks; ++cb) acc[cb] = f32x4{};
 
-  auto compute = [&](auto sc) {
+  // kv: elements of the stage below K, counted from its first k.  Under K
+  // (kv < kRsStep, only the last stage when K is not a multiple of 8) the
+  // DMA brought the whole chunk that straddles K: its elements past K (the
+  // next row, or row padding that may hold NaN) are cleared.  Lane l's
+  // fragment j holds k = 32j + 8(l/16) .. +7 of the stage.
+  auto compute = [&](auto sc, int kv) {
     constexpr int S = decltype(sc)::value;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const u32x4 af = *reinterpret_cast<const u32x4*>(rs_a<NB, S>() + fa[j]);
+      u32x4 af = *reinterpret_cast<const u32x4*>(rs_a<NB, S>() + fa[j]);
+      if constexpr (!UA) {
+        if (kv < kRsStep) {
+          const int v = min(max(kv - (32 * j + 8 * (lane >> 4)), 0), 8);
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            af[w] &= (2 * w < v ? 0x0000ffffu : 0u) | (2 * w + 1 < v ? 0xffff0000u : 0u);
+        }
+      }
 #pragma unroll
       for (int cb = 0; cb < kBlocks; ++cb) {
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -1876,7 +1889,9 @@ __global__ __launch_bounds__(NB == 64 ? 512 : 256) void gemm_rowstream_kernel(Ro
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     issue(StageC<(S + STAGES - 1) % STAGES>{}, step + STAGES - 1);
-    compute(sc);
+    int s_k = step + rot;
+    if (s_k >= nsteps) s_k -= nsteps;
+    compute(sc, g.K - (kbeg + s_k * kRsStep));
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -2606,12 +2621,13 @@ int run_skinny(const Scratch& sc, int dtype, const void* A, int64_t lda, const v
 // B's rows need not be aligned: B (at most 64 columns) is read in place by
 // the DMA when its last chunk is safely readable (chunk_tail_readable; the
 // chunk holding column N - 1 brings columns that reach only C columns >= N)
-// and repacked otherwise.  A goes by DMA when K is a multiple of 8 (no chunk
-// straddles K), its rows are 16-byte aligned or its last chunk is safely
-// readable, and its offsets stay below 2^31; through registers otherwise.
+// and repacked otherwise.  A goes by DMA when its rows are 16-byte aligned
+// or its last chunk is safely readable, and its offsets stay below 2^31
+// (the chunk straddling K is cleared past K in the fragments); through
+// registers otherwise.
 bool rowstream_a_dma(const void* A, int64_t lda, int64_t M, int64_t K) {
-  return K % 8 == 0 && ((int64_t)round_up(M, kRsRows) * lda + round_up(K, kRsStep)) * 2 < ((int64_t)1 << 31) &&
-         ((aligned16(A) && lda % 8 == 0) || (aligned2(A) && chunk_tail_readable(A, M, K, lda)));
+  return ((int64_t)round_up(M, kRsRows) * lda + round_up(K, kRsStep)) * 2 < ((int64_t)1 << 31) &&
+         ((aligned16(A) && lda % 8 == 0) || (K > 0 && aligned2(A) && chunk_tail_readable(A, M, K, lda)));
 }
 bool rowstream_b_in_place(const void* B, int64_t ldb, int64_t N, int64_t K) {
   return (aligned16(B) && ldb % 8 == 0) || (aligned2(B) && chunk_tail_readable(B, K, N, ldb));

@@ -545,17 +545,19 @@ def test_narrow_kernel_rejects_what_it_cannot_run():
 @pytest.mark.parametrize("m,n,k", [(100, 8, 257), (16384, 8, 16383), (4096, 13, 8191), (3000, 32, 4095),
                                    (777, 1, 9), (65, 17, 1), (2049, 24, 130)])
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
-def test_narrow_kernel_register_staged_a(m, n, k, dtype):
-    """A's rows not 16-byte aligned (K odd in a tight A, plus NaN row
-    padding beyond K in a view): A goes through registers in the narrow
-    kernel and elements at k >= K are cleared before they meet B."""
+def test_narrow_kernel_k_not_a_multiple_of_8(m, n, k, dtype):
+    """K not a multiple of 8 (odd K in a tight A, plus NaN row padding
+    beyond K in a view): the narrow kernel's DMA brings the chunk that
+    straddles K, and the fragments clear its elements at k >= K before they
+    meet B (A whose last chunk cannot be read safely goes through registers,
+    with the same clearing; see the HCG_UNALIGNED_DMA=0 test)."""
     import hc.gfx950 as g
     from hc.gfx950.workloads import make_inputs
 
     cfg = "c2_4096_f16" if dtype == "float16" else "c3_8192_bf16"
     a, b = make_inputs(cfg, seed=m + n + k, m=m, n=n, k=k)
     want = oracle.gemm_c(a, b, _dt(dtype))
-    print(f"case narrow register-staged A {dtype} m={m} n={n} k={k}", flush=True)
+    print(f"case narrow K tail {dtype} m={m} n={n} k={k}", flush=True)
     _check(_gemm(a, b, "narrow", dtype), want, k)
     tdt = torch.float16 if dtype == "float16" else torch.bfloat16
     big_a = torch.full((m, k + 5), float("nan"), dtype=tdt, device=DEV)
@@ -576,8 +578,8 @@ def test_narrow_kernel_register_staged_a(m, n, k, dtype):
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_narrow_kernel_64_columns(m, n, k, dtype):
     """33..64 columns: the narrow kernel's 64-column form (5-stage ring, A
-    and B of a stage in one 32 KB object), A by DMA or through registers
-    (odd K), C in a NaN guard band."""
+    and B of a stage in one 32 KB object), A by DMA (odd K: the chunk
+    straddling K cleared past K), C in a NaN guard band."""
     import hc.gfx950 as g
     from hc.gfx950.workloads import make_inputs
 
@@ -595,7 +597,7 @@ def test_narrow_kernel_64_columns(m, n, k, dtype):
     assert np.all(np.isnan(host[mask]))
 
 
-def test_narrow_kernel_register_staged_a_integer_bit_exact():
+def test_narrow_kernel_k_tail_integer_bit_exact():
     rng = np.random.default_rng(21)
     ai = rng.integers(-4, 5, size=(5000, 4095))
     bi = rng.integers(-4, 5, size=(4095, 11))
@@ -760,7 +762,8 @@ def test_paths_for_operands_the_dma_cannot_read():
         for m, n, k, pad_a, pad_b, algo in [(4095, 3001, 1027, 0, 0, "auto"), (601, 713, 1027, 9, 3, "tiled_256x192"),
                                             (16, 8191, 4096, 0, 0, "skinny"), (17, 50257, 1024, 0, 0, "skinny"),
                                             (64, 1001, 4096, 3, 0, "skinny"), (5, 7, 9, 0, 0, "skinny"),
-                                            (3000, 13, 4096, 0, 0, "narrow"), (300, 40, 1024, 3, 5, "narrow")]:
+                                            (3000, 13, 4096, 0, 0, "narrow"), (300, 40, 1024, 3, 5, "narrow"),
+                                            (4096, 13, 8191, 0, 0, "narrow"), (100, 8, 257, 5, 0, "narrow")]:
             for dt in (torch.float16, torch.bfloat16):
                 ai = rng.integers(-4, 5, size=(m, k)); bi = rng.integers(-4, 5, size=(k, n))
                 big_a = torch.full((m, k + pad_a), float("inf"), dtype=dt, device=dev)
