@@ -1467,11 +1467,25 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
 #pragma unroll
     for (int j = 0; j < kBlocks; ++j) acc[rb][j] = f32x4{};
 
-  auto compute = [&](auto sc) {
+  // kv: elements of the stage below K, counted from its first k.  Under K
+  // (kv < kStStep: the last stage, when K is not a multiple of 8) the chunk
+  // of A straddling K arrived whole; its elements past K (the next row, or
+  // row padding that may hold NaN) are cleared.  Lane l's fragment holds
+  // k = 8(l/16) .. +7 of the stage.
+  auto compute = [&](auto sc, int kv) {
     constexpr int S = decltype(sc)::value;
     u32x4 af[R];
 #pragma unroll
     for (int rb = 0; rb < R; ++rb) af[rb] = *reinterpret_cast<const u32x4*>(st_a<R, S>() + rb * kStABytes + fa);
+    if (kv < kStStep) {
+      const int v = min(max(kv - 8 * (lane >> 4), 0), 8);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t m = (2 * w < v ? 0x0000ffffu : 0u) | (2 * w + 1 < v ? 0xffff0000u : 0u);
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb) af[rb][w] &= m;
+      }
+    }
 #pragma unroll
     for (int j = 0; j < kBlocks; ++j) {
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -1519,7 +1533,7 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     issue(StageC<(S + PF) % kStStages>{}, step + PF);
-    compute(sc);
+    compute(sc, g.K - (kbeg + step * kStStep));
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -2483,24 +2497,23 @@ int launch_stream(const StreamArgs& a, hipStream_t stream) {
 int stream_rblocks(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8; }
 
 // The streaming kernel masks at 8-element granularity through the buffer
-// range check.  B, the streamed operand, needs 16-byte aligned rows; N need
-// not be a multiple of 8 (the chunk holding column N - 1 also loads up to 7
-// padding columns, which reach only output columns >= N, never stored).  A
-// (at most 128 rows) is used in place when its rows are aligned and K is a
-// multiple of 8, and otherwise repacked into zero-padded rows of
-// round_up(K, 8) (a chunk straddling K would pair A's row padding, possibly
-// Inf or NaN, with zeroed B rows).  Byte offsets stay below 2^31.
+// range check (chunks past the split's K range or past N, and rows past M,
+// load zeros).  N need not be a multiple of 8 (the chunk holding column
+// N - 1 also loads up to 7 padding columns, which reach only output columns
+// >= N, never stored).  A (at most 128 rows) and B are read in place where
+// that is safe (below); otherwise A is repacked into zero-padded rows of
+// round_up(K, 8) and B is register-staged (UB).  A's byte offsets stay
+// below 2^31.
 bool stream_extent_a(int64_t lda, int64_t M, int64_t K) {
   return ((int64_t)16 * stream_rblocks(M) * lda + K) * 2 < ((int64_t)1 << 31);
 }
 // The DMA reads 16-byte chunks at any 2-byte alignment: rows that are not
 // 16-byte aligned are read in place when the last chunk's bytes past the
-// operand stay in its last page (chunk_tail_readable).  A also needs K a
-// multiple of 8 (no chunk of A straddles K: this kernel does not clear
-// elements past K).
+// operand stay in its last page (chunk_tail_readable).  A chunk of A that
+// straddles K is cleared past K in the kernel's fragments.
 bool stream_a_in_place(const void* A, int64_t lda, int64_t M, int64_t K) {
-  return K % 8 == 0 && stream_extent_a(lda, M, K) &&
-         ((aligned16(A) && lda % 8 == 0) || (aligned2(A) && chunk_tail_readable(A, M, K, lda)));
+  return stream_extent_a(lda, M, (int64_t)round_up(K, 8)) &&
+         ((aligned16(A) && lda % 8 == 0) || (K > 0 && aligned2(A) && chunk_tail_readable(A, M, K, lda)));
 }
 bool stream_b_dma(const void* B, int64_t ldb, int64_t N, int64_t K) {
   return ((int64_t)round_up(K, kStStep) * ldb + round_up(N, kStN)) * 2 < ((int64_t)1 << 31) &&

@@ -418,10 +418,12 @@ def test_streaming_kernel_unaligned_a_in_place(m, n, k, pad):
 
 @pytest.mark.parametrize("m,n,k", [(16, 8192, 8191), (64, 2048, 4095), (128, 1000, 1001), (5, 4096, 2049)])
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
-def test_streaming_kernel_with_a_repacked(m, n, k, dtype):
-    """K not a multiple of 8 (A's rows unaligned): A is repacked into
-    zero-padded rows and B still streams through the DMA kernel; A's row
-    padding holds NaN."""
+def test_streaming_kernel_k_not_a_multiple_of_8(m, n, k, dtype):
+    """K not a multiple of 8 (A's rows unaligned): A is read in place, the
+    chunk straddling K cleared past K in the fragments, while A's row
+    padding holds NaN; B streams through the DMA.  (A whose last chunk
+    cannot be read safely is repacked instead: the HCG_UNALIGNED_DMA=0
+    test.)"""
     import hc.gfx950 as g
     from hc.gfx950.workloads import make_inputs
 
@@ -431,7 +433,7 @@ def test_streaming_kernel_with_a_repacked(m, n, k, dtype):
     big_a = torch.full((m, k + 3), float("nan"), dtype=tdt, device=DEV)
     big_a[:, :k] = _dev(a, dtype)
     out = torch.full((m, n), float("nan"), dtype=torch.float32, device=DEV)
-    print(f"case stream repacked A {dtype} m={m} n={n} k={k}", flush=True)
+    print(f"case stream K tail {dtype} m={m} n={n} k={k}", flush=True)
     g.gemm(big_a[:, :k], _dev(b, dtype), out=out, algo="skinny")
     torch.cuda.synchronize()
     _check(out.cpu().numpy(), oracle.gemm_c(a, b, _dt(dtype)), k)
@@ -761,6 +763,7 @@ def test_paths_for_operands_the_dma_cannot_read():
         rng = np.random.default_rng(5)
         for m, n, k, pad_a, pad_b, algo in [(4095, 3001, 1027, 0, 0, "auto"), (601, 713, 1027, 9, 3, "tiled_256x192"),
                                             (16, 8191, 4096, 0, 0, "skinny"), (17, 50257, 1024, 0, 0, "skinny"),
+                                            (16, 4096, 2049, 0, 0, "skinny"),
                                             (64, 1001, 4096, 3, 0, "skinny"), (5, 7, 9, 0, 0, "skinny"),
                                             (3000, 13, 4096, 0, 0, "narrow"), (300, 40, 1024, 3, 5, "narrow"),
                                             (4096, 13, 8191, 0, 0, "narrow"), (100, 8, 257, 5, 0, "narrow")]:

@@ -64,14 +64,14 @@ def _operands(m, n, k, lda, ldb, kind, seed):
 
 # (first call, second smaller call): (m, n, k, lda, ldb)
 PAIRS = [
-    # repacked A and B (unaligned rows) on the tiled kernel
+    # unaligned rows read in place on the tiled kernel (no scratch), then a smaller one
     ((4095, 3001, 1027, 1027, 3001), (1000, 700, 515, 515, 700)),
     # split-K partials on the streaming kernel, then fewer rows and columns
     ((16, 8192, 8192, 8192, 8192), (16, 4096, 4096, 4096, 4096)),
-    # repacked A plus partials (K not a multiple of 8): rows 65..128 on the
-    # tiled kernel, then 40 rows on the streaming kernel
+    # K not a multiple of 8, A read in place: rows 65..128 on the tiled
+    # kernel with split partials, then 40 rows on the streaming kernel
     ((100, 6000, 8191, 8191, 6000), (40, 3000, 4001, 4001, 3000)),
-    # narrow output: split partials of the narrow kernel (B repacked in the second call)
+    # narrow output: split partials of the narrow kernel (B rows unaligned in the second call)
     ((6000, 40, 8192, 8192, 40), (3000, 13, 4096, 4096, 13)),
     # tiled split-K partials (few tiles, long K), then a smaller one
     ((1024, 1024, 8192, 8192, 1024), (512, 512, 4096, 4096, 512)),
@@ -105,18 +105,19 @@ def test_noalloc_matches_hcg_gemm_on_two_calls(first, second, kind):
 
 def test_noalloc_rejects_a_call_beyond_its_scratch_before_any_launch():
     native, lib = _lib()
-    # 40 rows (the streaming kernel) with K not a multiple of 8: A is
+    # 40 rows (the streaming kernel, four 16-row blocks) with a row stride of
+    # 2^24 + 8 elements: in place its offsets would pass 2^31, so A is
     # repacked, 40 x 524296 x 2 bytes (42 MB), more than the 32 MiB array.
-    m, n, k = 40, 128, (1 << 19) + 1
-    _, _, ta, tb = _operands(m, n, k, k, n, "int", seed=5)
+    m, n, k, lda = 40, 128, (1 << 19) + 1, (1 << 24) + 8
+    _, _, ta, tb = _operands(m, n, k, lda, n, "int", seed=5)
     print("case noalloc over the scratch limit", flush=True)
-    rc, got, band = _call("hcg_gemm_noalloc", ta, k, tb, n, m, n, k)
+    rc, got, band = _call("hcg_gemm_noalloc", ta, lda, tb, n, m, n, k)
     assert rc == native.HCG_EINVAL
     msg = native.last_error(lib)
     assert "bytes of scratch" in msg and str(native.NOALLOC_SCRATCH_BYTES) in msg, msg
     assert band and np.isnan(got).all(), "a rejected call must not launch"
     # the same call through hcg_gemm (which allocates) works
-    rc, _, band = _call("hcg_gemm", ta, k, tb, n, m, n, k)
+    rc, _, band = _call("hcg_gemm", ta, lda, tb, n, m, n, k)
     native.check(lib, rc, "hcg_gemm")
     assert band
 
