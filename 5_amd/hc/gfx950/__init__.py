@@ -197,12 +197,13 @@ def gemm(a: Any, b: Any, out: Any | None = None, *, algo: str = "auto", device: 
     returns after the result is on the host.
 
     ``algo``: "auto" (the library picks: the narrow streaming kernel for
-    N <= 64, A by DMA when its rows are 16-byte aligned and through
-    registers otherwise; else the streaming kernel for M <= 128, B by DMA
-    or through registers likewise;
-    otherwise the LDS-tiled kernel with a modelled tile shape and K split,
-    with up to 128 rows or 64 columns past a multiple of 256 peeled off to
-    a streaming kernel when that saves a round of tiles),
+    N <= 64; the streaming kernel for M <= 64, and for M <= 128 when the
+    tiled kernel cannot read B in place; otherwise the LDS-tiled kernel
+    with a modelled tile shape and K split, with up to 128 rows or 64
+    columns past a multiple of 256 peeled off to a streaming kernel when
+    that saves a round of tiles.  Operands are read in place at any row
+    alignment; one whose last 16-byte piece cannot be read safely is
+    repacked, or goes through registers),
     "tiled", "skinny", "narrow", "generic", or a fixed tile shape
     "tiled_256x256", "tiled_256x192", "tiled_128x256", "tiled_128x128",
     "tiled_256x64" (never split along K).

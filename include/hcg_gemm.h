@@ -57,8 +57,9 @@ extern "C" {
 #define HCG_ALGO_TILED_128x128 7
 #define HCG_ALGO_TILED_256x64 8
 /* Streaming kernel for N <= 64 (A streamed once in 256-byte row pieces, K split to fill the
- * chip; HBM-bound shapes).  Any layout: A by DMA when its rows are 16-byte aligned and K is a
- * multiple of 8, through registers otherwise; B repacked when its rows are not aligned. */
+ * chip; HBM-bound shapes).  Any layout: A and B read in place by DMA at any row alignment; an
+ * operand whose last 16-byte piece cannot be read safely goes through registers (A) or is
+ * repacked (B). */
 #define HCG_ALGO_NARROW 9
 
 /* Idempotent one-time set-up (device properties).  Replaces the reference's
@@ -88,11 +89,12 @@ int hcg_gemm_algo(int algo, int dtype, const void* A, int64_t lda, const void* B
  * library call on any path, for callers that cannot allocate (code under
  * HIP graph capture, tight serving loops, harnesses that forbid it).  No
  * counterpart in the reference, which has no launch ABI.  Scratch
- * (operands repacked when their rows are not 16-byte aligned, split-K
- * partials) comes from one static device array of HCG_NOALLOC_SCRATCH_BYTES
+ * (split-K partials, and operands repacked when they cannot be read in
+ * place) comes from one static device array of HCG_NOALLOC_SCRATCH_BYTES
  * per GPU, held from the library's first use on that GPU until the process
  * ends; K splits are limited to what fits, and a call that still needs more
- * (large unaligned operands) fails with HCG_EINVAL before any launch.  Every
+ * (a large operand that must be repacked) fails with HCG_EINVAL before any
+ * launch.  Every
  * call on one GPU shares that array: calls that overlap in time on one GPU
  * (other streams, other host threads, concurrent graph replays) race, so
  * the caller must order them.  Nothing in the array needs to start at zero:
