@@ -170,15 +170,18 @@ def _torch():
 
 
 def _check_shapes(a: Any, b: Any, c: Any | None) -> tuple[int, int, int]:
-    if len(a.shape) != 2 or len(b.shape) != 2:
+    sa, sb = a.shape, b.shape
+    if len(sa) != 2 or len(sb) != 2:
         raise LaunchError("A and B must be rank-2 matrices")
-    m, k = int(a.shape[0]), int(a.shape[1])
-    k2, n = int(b.shape[0]), int(b.shape[1])
+    m, k = sa
+    k2, n = sb
     if k != k2:
         raise LaunchError("A.shape[1] must match B.shape[0]")
-    if c is not None and tuple(int(d) for d in c.shape) != (m, n):
-        raise LaunchError(f"C shape {tuple(c.shape)} does not match ({m}, {n})")
-    return m, n, k
+    if c is not None:
+        sc = c.shape
+        if len(sc) != 2 or sc[0] != m or sc[1] != n:
+            raise LaunchError(f"C shape {tuple(sc)} does not match ({m}, {n})")
+    return int(m), int(n), int(k)
 
 
 def _dtype_code(a: Any, b: Any) -> int:
@@ -277,6 +280,8 @@ def _current_device(torch: Any) -> int:
 
 
 def _gemm_torch(torch: Any, a: Any, b: Any, out: Any | None, algo: int) -> Any:
+    # (A call costs a few microseconds of host time, about as long as a
+    # small GEMM's kernel: each tensor attribute is read once.)
     m, n, k = _check_shapes(a, b, out)
     index = a.get_device()  # -1 on the CPU
     ib, io = b.get_device(), (index if out is None else out.get_device())
@@ -284,7 +289,10 @@ def _gemm_torch(torch: Any, a: Any, b: Any, out: Any | None, algo: int) -> Any:
         raise LaunchError("torch tensors must live on a GPU")
     if ib != index or io != index:
         raise LaunchError("A, B and C must live on the same device")
-    dtype = _torch_dtype_code(torch, a, b)
+    dta = a.dtype
+    dtype = _TORCH_DTYPE_CODES.get(dta) if _TORCH_DTYPE_CODES else None
+    if dtype is None or b.dtype is not dta:
+        dtype = _torch_dtype_code(torch, a, b)
     if out is None:
         out = torch.empty((m, n), dtype=torch.float32, device=a.device)
     elif out.dtype != torch.float32:
@@ -307,8 +315,11 @@ def _gemm_torch(torch: Any, a: Any, b: Any, out: Any | None, algo: int) -> Any:
     ldb = max(sb[0], n) if k > 1 else max(n, 1)
     ldc = max(st[0], n) if m > 1 else max(n, 1)
     if _current_device(torch) == index:
-        _native.gemm(algo, dtype, a.data_ptr(), lda, b.data_ptr(), ldb, target.data_ptr(), ldc, m, n, k,
-                     _current_stream(torch, index))
+        lib = _native.lib()
+        rc = lib.hcg_gemm_algo(algo, dtype, a.data_ptr(), lda, b.data_ptr(), ldb, target.data_ptr(), ldc, m, n, k,
+                               _current_stream(torch, index) or None)
+        if rc:
+            _native.check(lib, rc, "hcg_gemm")
     else:
         with torch.cuda.device(index):
             _native.gemm(algo, dtype, a.data_ptr(), lda, b.data_ptr(), ldb, target.data_ptr(), ldc, m, n, k,

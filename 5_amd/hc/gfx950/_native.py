@@ -131,6 +131,11 @@ def check(lib: ctypes.CDLL, rc: int, what: str) -> None:
     raise BackendError(f"{what} failed ({rc}): {msg}")
 
 
+def lib() -> ctypes.CDLL:
+    """The loaded library (loading it on first use)."""
+    return _lib if _lib is not None else load()
+
+
 def gemm(
     algo: int,
     dtype: int,
