@@ -712,6 +712,11 @@ def test_unaligned_strided_views_against_oracle(m, n, k, pad_a, pad_b):
         (257, 129, 31, 7, 0, "tiled_256x256", "bfloat16"),
         (64, 200, 13, 3, 3, "tiled_128x256", "float16"),
         (700, 64, 2049, 5, 1, "tiled_256x64", "float16"),
+        # 65..128 rows with B's rows unaligned: AUTO sends them to the tiled
+        # kernel (split along K), which reads B in place
+        (128, 3001, 1027, 0, 0, "auto", "float16"),
+        (100, 5001, 1024, 3, 0, "auto", "bfloat16"),
+        (72, 1229, 4096, 0, 1, "auto", "float16"),
     ],
 )
 def test_unaligned_rows_read_in_place(m, n, k, pad_a, pad_b, algo, dtype):
