@@ -7,7 +7,10 @@ declared in include/hcg_gemm.h and include/hcg_tile_ops.h) with hipcc for
 gfx950 into
 5_amd/hc/gfx950/libhcg_gfx950.so, next to the Python code that loads it,
 and hcg_probe.hip (the hardware ceiling probes of include/hcg_probe.h, used
-by bench.py) into 5_amd/hc/gfx950/libhcg_probe.so.
+by bench.py) into 5_amd/hc/gfx950/libhcg_probe.so, and hcg_torch.cpp (host
+code: the device-tensor binding of hcg_gemm_algo as a Python extension,
+linked against libhcg_gfx950.so) with g++ against the installed PyTorch into
+5_amd/hc/gfx950/_hcg_torch<EXT_SUFFIX>.
 hipcc cross-compiles, so this runs on a machine without a GPU.
 """
 
@@ -17,6 +20,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
@@ -26,6 +30,8 @@ INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(PKG, "hc", "gfx950", "libhcg_gfx950.so")
 PROBE_SRCS = [os.path.join(HERE, "hcg_probe.hip")]
 PROBE_OUT = os.path.join(PKG, "hc", "gfx950", "libhcg_probe.so")
+TORCH_SRC = os.path.join(HERE, "hcg_torch.cpp")
+TORCH_OUT = os.path.join(PKG, "hc", "gfx950", "_hcg_torch" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 ARCH = "gfx950"
 
 
@@ -72,10 +78,34 @@ def _compile(srcs: list[str], out: str, verbose: bool) -> str:
     return out
 
 
+def _compile_torch_binding(verbose: bool) -> str:
+    """g++ on hcg_torch.cpp: PyTorch's headers and libraries, the HIP headers
+    (host code only), and libhcg_gfx950.so found next to the module."""
+    import torch.utils.cpp_extension as cpp
+
+    tmp = TORCH_OUT + ".tmp"
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__",
+           "-DTORCH_EXTENSION_NAME=_hcg_torch", "-DTORCH_API_INCLUDE_EXTENSION_H", "-D_GLIBCXX_USE_CXX11_ABI=1",
+           *(f"-I{p}" for p in cpp.include_paths()), f"-I{sysconfig.get_paths()['include']}",
+           "-I/opt/rocm/include", f"-I{INCLUDE}", TORCH_SRC, "-o", tmp,
+           *(f"-L{p}" for p in cpp.library_paths()), "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
+           "-ltorch_python", f"-L{os.path.dirname(OUT)}", "-l:libhcg_gfx950.so", "-Wl,-rpath,$ORIGIN",
+           *(f"-Wl,-rpath,{p}" for p in cpp.library_paths())]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"g++ failed ({proc.returncode}):\n{proc.stderr}")
+    os.replace(tmp, TORCH_OUT)
+    return TORCH_OUT
+
+
 def build(verbose: bool = False) -> str:
-    """Builds the GEMM library and the probe library; returns the former."""
+    """Builds the GEMM library, the probe library and the device-tensor
+    binding; returns the first."""
     out = _compile(SRCS, OUT, verbose)
     _compile(PROBE_SRCS, PROBE_OUT, verbose)
+    _compile_torch_binding(verbose)
     return out
 
 

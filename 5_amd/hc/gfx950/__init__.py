@@ -279,7 +279,35 @@ def _current_device(torch: Any) -> int:
     return _CUR_DEVICE()
 
 
+_FAST: Any = None  # _hcg_torch.gemm once loaded; False when the binding is not built
+
+
+def _fast_gemm() -> Any:
+    """The compiled device-tensor binding (_hcg_torch, built beside the
+    library): the common case's checks and launch in C++, without the
+    Python attribute reads below.  It runs the same library; where it is
+    not built, the ctypes path below runs instead."""
+    global _FAST
+    if _FAST is None:
+        _native.load()  # the library first: the binding links against it
+        try:
+            from . import _hcg_torch
+        except ImportError:
+            _FAST = False
+        else:
+            _FAST = _hcg_torch.gemm
+    return _FAST
+
+
 def _gemm_torch(torch: Any, a: Any, b: Any, out: Any | None, algo: int) -> Any:
+    if out is not None:
+        fast = _FAST if _FAST is not None else _fast_gemm()
+        if fast:
+            rc = fast(a, b, out, algo)  # -1: a case the binding leaves to the path below
+            if rc == 0:
+                return out
+            if rc > 0:
+                _native.check(_native.lib(), rc, "hcg_gemm")
     # (A call costs a few microseconds of host time, about as long as a
     # small GEMM's kernel: each tensor attribute is read once.)
     m, n, k = _check_shapes(a, b, out)

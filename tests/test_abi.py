@@ -106,3 +106,14 @@ def test_tile_ops_with_nothing_to_do_launch_nothing():
     assert lib.hcg_tile_store(8, None, 0, 0, 0, 0x1000, 2, 2, 2, 0x1000, None, None) == _native.HCG_OK
     assert lib.hcg_tile_store(2, 0x1000, 4, 4, 4, 0x1000, 1, 2, 2, None, None, None) == _native.HCG_EINVAL
     assert "tiles is NULL" in _native.last_error(lib)
+
+
+def test_device_tensor_binding_is_built_and_leaves_other_cases_to_python():
+    """_hcg_torch (the compiled binding of hcg_gemm_algo for device tensors)
+    is built beside the library and returns -1, launching nothing, for
+    tensors it does not take (here CPU tensors)."""
+    torch = pytest.importorskip("torch")
+    from hc.gfx950 import _hcg_torch
+
+    a = torch.zeros((4, 4), dtype=torch.float16)
+    assert _hcg_torch.gemm(a, a, torch.zeros((4, 4)), 0) == -1

@@ -1179,3 +1179,37 @@ def test_wide_a_operand_over_2gib_bit_exact():
     got = c.cpu().numpy()
     for i in range(7):
         assert np.array_equal(got[i::7], np.broadcast_to(rows[i], got[i::7].shape)), f"rows = {i} mod 7"
+
+
+@pytest.mark.parametrize("m,n,k,dtype", [(128, 128, 128, "float16"), (4095, 3001, 1027, "float16"),
+                                         (16, 8192, 8192, "bfloat16"), (3000, 13, 4096, "float16")])
+def test_compiled_binding_matches_the_ctypes_path(m, n, k, dtype):
+    """hc.gfx950.gemm on device tensors goes through the compiled binding
+    (_hcg_torch); the ctypes call of the same entry point gives the same
+    bits, and a case the binding leaves to Python (a transposed view of B)
+    still runs through the general path."""
+    import hc.gfx950 as g
+    from hc.gfx950 import _hcg_torch, _native
+    from hc.gfx950.workloads import make_inputs
+
+    print(f"case compiled binding {dtype} m={m} n={n} k={k}", flush=True)
+    a, b = make_inputs("c2_4096_f16" if dtype == "float16" else "c3_8192_bf16", seed=m + n, m=m, n=n, k=k)
+    ta, tb = _dev(a, dtype), _dev(b, dtype)
+    via_binding = torch.full((m, n), float("nan"), dtype=torch.float32, device=DEV)
+    assert _hcg_torch.gemm(ta, tb, via_binding, _native.HCG_ALGO_AUTO) == 0
+    via_ctypes = torch.full((m, n), float("nan"), dtype=torch.float32, device=DEV)
+    lib = _native.load()
+    rc = lib.hcg_gemm_algo(_native.HCG_ALGO_AUTO, _native.HCG_F16 if dtype == "float16" else _native.HCG_BF16,
+                           ta.data_ptr(), k, tb.data_ptr(), n, via_ctypes.data_ptr(), n, m, n, k,
+                           torch.cuda.current_stream().cuda_stream)
+    _native.check(lib, rc, "hcg_gemm_algo")
+    via_wrapper = g.gemm(ta, tb, out=torch.empty((m, n), dtype=torch.float32, device=DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(via_binding, via_ctypes) and torch.equal(via_wrapper, via_ctypes)
+    _check(via_binding.cpu().numpy(), oracle.gemm_c(a, b, _dt(dtype)), k)
+    tbt = tb.t().contiguous().t()  # column-major B: the binding declines, the wrapper copies it
+    out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    assert _hcg_torch.gemm(ta, tbt, out, _native.HCG_ALGO_AUTO) == -1
+    g.gemm(ta, tbt, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, via_ctypes)
