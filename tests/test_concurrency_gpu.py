@@ -5,13 +5,14 @@ The reference runs concurrent launches from two threads
 through the C ABI.  Graph capture: the kernels take no host-side action
 inside a launch except on a stream's first use of a workspace size (an
 allocation), so after one warm-up call on the capture stream every path --
-tiled, skinny split-K (workspace partials + reduce), tiled split-K,
-repacked ragged operands (workspace copies), the narrow kernel (repacked
-B, split partials), a peeled shape (tiled bulk + streaming remainder, two
-launches sharing the workspace) and the register-staged streaming forms
-(unaligned B rows; unaligned A rows in the narrow kernel) -- records into a
-graph.  Every replay is
-checked against the eager result, with eager work between replays.
+tiled, skinny split-K (workspace partials + reduce), tiled split-K, ragged
+operands read in place, the narrow kernel (split partials), a peeled shape
+(tiled bulk + streaming remainder, two launches sharing the workspace),
+unaligned B rows and odd K on the streaming kernels -- records into a
+graph; and, in a process that turns in-place reads of unaligned rows off,
+so do the repack kernel and the register-staged streaming forms.  Every
+replay is checked against the eager result, with eager work between
+replays.
 """
 
 from __future__ import annotations
@@ -43,15 +44,15 @@ CASES = [
     ("splitk", 512, 512, 16384),
     ("narrow", 2048, 13, 4096),
     ("peel", 4111, 4096, 1024),
-    ("staged_b", 16, 8191, 4096),
-    ("staged_a", 4096, 40, 4095),
+    ("unaligned_b", 16, 8191, 4096),
+    ("odd_k_narrow", 4096, 40, 4095),
 ]
 
 
 def _inputs(name, m, n, k, seed):
     from hc.gfx950.workloads import make_inputs
 
-    cfg = "c4_skinny_f16" if name in ("skinny", "staged_b") else "c2_4096_f16"
+    cfg = "c4_skinny_f16" if name in ("skinny", "unaligned_b") else "c2_4096_f16"
     return make_inputs(cfg, seed=seed, m=m, n=n, k=k)
 
 
@@ -163,6 +164,60 @@ def test_graph_capture_replays_match_eager(name, m, n, k):
     for i, o in enumerate(outs2):
         rep = oracle.parity_check(o.cpu().numpy(), want2, k)
         assert rep.ok, f"eager call {i}: {rep}"
+
+
+def test_graph_capture_of_the_repack_and_register_staged_paths():
+    """With HCG_UNALIGNED_DMA=0 (a fresh process: the library reads it
+    once) unaligned rows take the fallback paths: A and B repacked into the
+    workspace before the tiled kernel, B register-staged in the streaming
+    kernel, A register-staged and B repacked in the narrow kernel.  Each is
+    captured after a warm-up call and replayed, with eager calls on other
+    operands on the capturing stream between replays."""
+    import os
+    import subprocess
+    import sys
+    import textwrap
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    script = textwrap.dedent(f"""
+        import sys
+        sys.path[:0] = [{os.path.join(root, "5_amd")!r}, {os.path.join(root, "oracle")!r}]
+        import torch
+        import hc.gfx950 as g, hc_oracle as oracle
+        from hc.gfx950.workloads import make_inputs, to_torch
+        dev = torch.device("cuda:0")
+        for name, m, n, k in [("repacked", 1000, 601, 333), ("staged_b", 16, 8191, 4096),
+                              ("staged_a", 4096, 13, 4095), ("narrow_repacked_b", 2048, 40, 4095)]:
+            print("case graph fallback", name, m, n, k, flush=True)
+            a, b = make_inputs("c2_4096_f16", seed=7, m=m, n=n, k=k)
+            ta, tb = to_torch(a, "float16", dev), to_torch(b, "float16", dev)
+            out = torch.empty((m, n), dtype=torch.float32, device=dev)
+            s = torch.cuda.Stream(device=dev)
+            with torch.cuda.stream(s):
+                g.gemm(ta, tb, out=out)
+            s.synchronize()
+            eager = out.clone()
+            assert oracle.parity_check(eager.cpu().numpy(), oracle.gemm_c(a, b), k).ok, name
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=s):
+                g.gemm(ta, tb, out=out)
+            a2, b2 = make_inputs("c2_4096_f16", seed=8, m=m, n=n, k=k)
+            ta2, tb2 = to_torch(a2, "float16", dev), to_torch(b2, "float16", dev)
+            want2 = oracle.gemm_c(a2, b2)
+            for i in range(3):
+                out.fill_(float("nan"))
+                torch.cuda.synchronize()
+                with torch.cuda.stream(s):
+                    o2 = g.gemm(ta2, tb2)
+                graph.replay()
+                torch.cuda.synchronize()
+                assert torch.equal(out, eager), (name, i)
+                assert oracle.parity_check(o2.cpu().numpy(), want2, k).ok, (name, i)
+    """)
+    print("case graph capture with HCG_UNALIGNED_DMA=0", flush=True)
+    env = dict(os.environ, HCG_UNALIGNED_DMA="0")
+    proc = subprocess.run([sys.executable, "-c", script], env=env, capture_output=True, text=True, timeout=110)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
 
 
 def test_graph_replays_stay_valid_after_the_stream_needs_a_larger_workspace():

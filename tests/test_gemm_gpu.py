@@ -442,7 +442,7 @@ def test_streaming_kernel_k_not_a_multiple_of_8(m, n, k, dtype):
 # Few output tiles and a long K: the tiled kernel splits K over several
 # workgroups per tile and sums their partials in a fixed order.  Shapes
 # include ragged M/N tails, a last split shorter than the others, unaligned
-# rows (repacked operands feeding the split) and bf16.
+# rows (read in place by every split) and bf16.
 SPLITK_SHAPES = [(1024, 1024, 8192), (512, 512, 16384), (700, 900, 12000), (200, 8000, 8200), (1500, 1500, 4104),
                  (333, 444, 9999), (1024, 4096, 16384)]
 
@@ -649,8 +649,8 @@ def test_runs_are_bit_identical(algo, m):
 
 
 # Operands whose rows are not 16-byte aligned (odd K or N, odd row strides,
-# 2-byte aligned starts), forced onto 256x192 tiles: the repack's zero
-# padding must cover every tail (K and N down to 1 element past a chunk).
+# 2-byte aligned starts), forced onto 256x192 tiles and read in place: no
+# element past K or N may reach C (K and N down to 1 element past a chunk).
 UNALIGNED_SHAPES = [(601, 713, 1027), (513, 200, 353), (300, 8, 5), (300, 9, 1), (17, 8, 1), (40, 8, 352),
              (257, 193, 320), (600, 1001, 2049), (300, 7, 40)]
 
@@ -659,7 +659,7 @@ UNALIGNED_SHAPES = [(601, 713, 1027), (513, 200, 353), (300, 8, 5), (300, 9, 1),
 @pytest.mark.parametrize("m,n,k", UNALIGNED_SHAPES)
 def test_unaligned_operands_integer_bit_exact(m, n, k, dtype):
     """Small-integer inputs make every summation order exact, so the
-    repacked operands must give A @ B bit for bit, tails included."""
+    unaligned operands must give A @ B bit for bit, tails included."""
     rng = np.random.default_rng(m * 7 + n * 3 + k)
     ai = rng.integers(-4, 5, size=(m, k))
     bi = rng.integers(-4, 5, size=(k, n))
@@ -841,7 +841,7 @@ def test_k_zero_writes_zeros_and_empty_output_is_untouched():
 
 def test_two_streams_use_separate_workspaces():
     """The split-K workspace is per stream: two streams running skinny GEMMs
-    (and repacks) concurrently must not corrupt each other."""
+    concurrently must not corrupt each other."""
     import hc.gfx950 as g
     from hc.gfx950.workloads import make_inputs
 
@@ -871,9 +871,10 @@ def test_numpy_bf16_is_not_accepted_and_launch_errors_surface():
 
 
 # Seeded random shapes, layouts and kernel choices against the oracle: every
-# path (tiled with and without a K split, repacked operands, the streaming
-# kernel at every row-block count, the narrow kernel, the register-staged
-# skinny fallback and the generic kernel) on shapes nobody picked by hand,
+# path (tiled with and without a K split, unaligned operands read in place,
+# the streaming kernel at every row-block count, the narrow kernel, the
+# register-staged skinny fallback and the generic kernel) on shapes nobody
+# picked by hand,
 # with NaN in the operands' row padding and around C.
 _RANDOM_ALGOS = ["auto", "auto", "auto", "tiled", "skinny", "generic", "tiled_128x128", "tiled_256x192"]
 
@@ -1147,8 +1148,9 @@ def test_streaming_kernel_any_n_with_nan_padding(m, n, k, dtype):
 @pytest.mark.parametrize("m,n,k", [(4100, 4096, 1024), (4096, 4104, 1024), (4111, 4096, 1025)])
 def test_remainder_peel_integer_bit_exact(m, n, k):
     """Exact sums, so the peeled and unpeeled results must agree bit for
-    bit; 4111 x 4096 x 1025 has unaligned rows of A (the bulk repacked, the
-    15 remainder rows on the register-staged kernel)."""
+    bit; 4111 x 4096 x 1025 has unaligned rows of A and K not a multiple of
+    8 (read in place by the bulk and by the 15 remainder rows on the
+    streaming kernel)."""
     rng = np.random.default_rng(m + n + k)
     ai = rng.integers(-4, 5, size=(m, k))
     bi = rng.integers(-4, 5, size=(k, n))
