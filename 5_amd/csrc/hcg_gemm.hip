@@ -13,31 +13,35 @@
 //     256-thread workgroup (256x256, 256x192, 128x256, 128x128 or 256x64, picked by
 //     size; 4 waves in 2x2, each (TM/2) x (TN/2) of MFMA 32x32x16 tiles),
 //     K step 32 through an LDS ring filled by direct global->LDS DMA loads
-//     (buffer_load ... lds), B kept row-major in LDS and read with
-//     transposing LDS loads (ds_read_b64_tr_b16), XOR-swizzled
-//     bank-conflict-free layouts, XCD-aware tile order, masked M/N/K tails
-//     by the buffer range check, and an LDS-staged 16-byte epilogue; shapes
-//     with few tiles and a long K split K over workgroups (partials summed
-//     in a fixed order by stream_reduce_kernel).
+//     (buffer_load ... lds; 256-row tiles move A two K steps at a time),
+//     operand rows read in place at any 2-byte alignment, B kept row-major
+//     in LDS and read with transposing LDS loads (ds_read_b64_tr_b16),
+//     XOR-swizzled bank-conflict-free layouts, XCD-aware tile order, masked
+//     M/N/K tails by the buffer range check (and the A elements past K
+//     cleared in the last K tile), and an LDS-staged 16-byte epilogue;
+//     shapes with few tiles and a long K split K over workgroups (partials
+//     summed in a fixed order by stream_reduce_kernel).
 //   * gemm_stream_kernel -- M <= 128, N > 64 (HBM-bound).  B streams HBM ->
-//     LDS once, by DMA or (rows not 16-byte aligned) through registers,
-//     split over K across workgroups mapped so every XCD covers all column
-//     residues, against 1, 2, 4 or 8 16-row blocks of A (repacked when
-//     needed); the split partials are summed in a fixed order
-//     (deterministic) by stream_reduce_kernel, skinny_reduce_kernel or,
-//     past 16 splits, split_reduce_kernel.
+//     LDS once by DMA, split over K across workgroups mapped so every XCD
+//     covers all column residues, against 1, 2, 4 or 8 16-row blocks of A;
+//     the split partials are summed in a fixed order (deterministic) by
+//     the last workgroup of each column block to arrive (R <= 2) or by
+//     stream_reduce_kernel, skinny_reduce_kernel or, past 16 splits,
+//     split_reduce_kernel.  Its UB form stages B through registers when
+//     B's last row piece cannot be read safely in place.
 //   * gemm_generic_kernel -- fallback (plain pointers, register staging, any
 //     alignment) for unaligned operands whose byte offsets do not fit 31
 //     bits; aligned ones that large run the DMA kernel's WIDE form.
 //   * gemm_rowstream_kernel -- N <= 64, any layout (HBM-bound): A streams
-//     HBM -> LDS once in 256-byte row pieces, by DMA or through registers,
-//     split over K; partials reduced as for gemm_stream_kernel.
+//     HBM -> LDS once in 256-byte row pieces, by DMA in place (through
+//     registers when its last row piece cannot be read safely), split over
+//     K; partials reduced as for gemm_stream_kernel.
 //   * gemm_skinny_kernel -- M <= 16 when the streaming kernels cannot take
 //     the operands: B streamed with 128-bit loads, transposed 8x8 in
 //     registers, split over K; partial sums reduced in a fixed order.
-//   * repack_kernel -- copies operands whose rows are not 16-byte aligned
-//     (or, for A, whose K is not a multiple of 8) into zero-padded aligned
-//     rows for the DMA kernels.
+//   * repack_kernel -- copies an operand that cannot be read in place (its
+//     last row piece not safely readable, or its offsets past 2^31) into
+//     zero-padded 16-byte aligned rows for the DMA kernels.
 //
 // Numerics: products of fp16/bf16 values are exact in float32 and the MFMA
 // accumulates in float32; only the order of the float32 additions differs
