@@ -295,7 +295,7 @@ __global__ __launch_bounds__(kTiledThreads) void gemm_generic_kernel(TiledArgs g
 }
 
 // ---------------------------------------------------------------------------
-// Fast tiled kernel (buffer loads; 16-byte aligned rows; offsets < 2^31)
+// Fast tiled kernel (LDS DMA; rows at any 2-byte alignment; offsets < 2^31)
 // ---------------------------------------------------------------------------
 
 struct FastArgs {
@@ -340,10 +340,12 @@ constexpr int kSgDsRead = 0x100;
 // point at 4 consecutive k rows x 16 columns, so lane i receives 4
 // consecutive k of column i, the MFMA B operand.
 //
-// Requirements (checked on the host): A, B 16-byte aligned; lda, ldb, K
-// multiples of 8 (or operands repacked to that form with zero padding).  N
-// need not be: the chunk holding column N - 1 also loads up to 7 padding
-// columns of B, which reach only C columns >= N (never stored).  Chunks past
+// Requirements (checked on the host): A and B readable in place (rows at
+// any 2-byte alignment, the bytes the last chunk reads past an operand
+// safely mapped; otherwise repacked into zero-padded aligned rows).  K and N
+// need not be multiples of 8: the chunk holding column N - 1 also loads up
+// to 7 padding columns of B, which reach only C columns >= N (never
+// stored), and the KT form clears A's elements past K.  Chunks past
 // K or N are redirected past the buffer extent, so the hardware range check
 // returns zeros; rows past M (A) or K (B) are past it already.
 
@@ -1143,7 +1145,7 @@ struct StreamArgs {
   const uint16_t* B;
   float* C;
   float* ws;      // [splits][16 * row blocks][N] partial sums (splits > 1)
-  int lda, ldb;   // elements; lda a multiple of 8, ldb too unless B is register-staged
+  int lda, ldb;   // elements (any pitch: rows are read at any 2-byte alignment)
   int64_t ldc;
   int M, N, K;
   int kchunk;     // rows per split, multiple of kStStep
@@ -1314,9 +1316,9 @@ __device__ __forceinline__ void stream_fused_reduce(const StreamArgs& g, const f
     }
 }
 
-// UB (B's rows not 16-byte aligned, so no DMA for B): each lane fetches the
-// two aligned 16-byte blocks around its B chunk PF stages ahead
-// into a register set of its own, and writes the chunk (shift_join of the
+// UB (B's last row piece not safely readable in place, so no DMA for B):
+// each lane fetches the two aligned 16-byte blocks around its B chunk PF
+// stages ahead into a register set of its own, and writes the chunk (shift_join of the
 // two) just before that stage's barrier to the LDS bytes the DMA would have
 // filled.  Every lane issues two loads per chunk (the wait counts double the
 // B part): chunks past N or rows past the split's K range read B's first
@@ -1616,9 +1618,10 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
 // MFMA 16x16x32: A fragments by ds_read_b128 (row l%16, 8 k at chunk l/16,
 // chunks XOR-swizzled by row), B fragments by two transposing reads as in
 // the skinny streaming kernel.  Rows past M, k past the run and columns
-// past N load as zero (range check or redirect); K must be a multiple of 8
-// (a chunk straddling K would pair k >= K of A with zeroed B rows), N need
-// not be (the straddling chunk's extra columns only reach C columns >= N).
+// past N load as zero (range check or redirect); K need not be a multiple
+// of 8 (the chunk straddling K is cleared past K in the last stage's
+// fragments), nor N (the straddling chunk's extra columns only reach C
+// columns >= N).
 
 constexpr int kRsRows = 64;
 constexpr int kRsStep = 128;
@@ -1695,12 +1698,13 @@ __device__ __forceinline__ unsigned char* rs_b() {
   }
 }
 
-// UA (A's rows not 16-byte aligned or K not a multiple of 8, so no DMA for
-// A): each lane loads the two aligned 16-byte blocks around its A chunk
+// UA (A's last row piece not safely readable in place, so no DMA for A):
+// each lane loads the two aligned 16-byte blocks around its A chunk
 // kRsStages - 1 stages ahead into registers, and just before the stage's
 // barrier writes the funnel-shifted chunk, elements at k >= K cleared (the
 // row padding may hold Inf or NaN), to the LDS bytes the DMA would fill.  B
-// (16-byte aligned rows, repacked when needed) comes through registers too:
+// (in place, or repacked when its last piece is not readable) comes through
+// registers too:
 // with an LDS DMA in flight the compiler waits for it, and so for every
 // older load, before LDS reads.  A second block past A's last byte is
 // replaced by the first (its bytes are k >= K, cleared).
@@ -2523,8 +2527,8 @@ bool stream_b_dma(const void* B, int64_t ldb, int64_t N, int64_t K) {
   return ((int64_t)round_up(K, kStStep) * ldb + round_up(N, kStN)) * 2 < ((int64_t)1 << 31) &&
          ((aligned16(B) && ldb % 8 == 0) || (aligned2(B) && chunk_tail_readable(B, K, N, ldb)));
 }
-// B that the DMA cannot take (rows not 16-byte aligned, or offsets past
-// 2^31) is register-staged: 16-byte loads at any 2-byte alignment, all
+// B that the DMA cannot take (last chunk not safely readable, or offsets
+// past 2^31) is register-staged: 16-byte loads at any 2-byte alignment, all
 // inside B's extent, which must then hold at least 8 elements.
 bool stream_fits(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N, int64_t K) {
   return M <= 16 * kStMaxRowBlocks && ldb < ((int64_t)1 << 31) &&
@@ -2825,8 +2829,8 @@ int run_tiled(const Scratch& sc, int dtype, const void* A, int64_t lda, const vo
     return dtype == HCG_F16 ? launch_dma<HCG_F16, true>(f, plan.shape, stream)
                             : launch_dma<HCG_BF16, true>(f, plan.shape, stream);
   }
-  // Workspace: repacked operands (rows not 16-byte aligned), then the split
-  // partials [splits][M][N].
+  // Workspace: repacked operands (those that cannot be read in place), then
+  // the split partials [splits][M][N].
   const size_t a_sz = a_ok ? 0 : round_up((size_t)M * lda_p * 2, 256);
   const size_t b_sz = b_ok ? 0 : round_up((size_t)K * ldb_p * 2, 256);
   // Explicit tile shapes run without a K split; "auto" and "tiled" may split.
@@ -2844,7 +2848,7 @@ int run_tiled(const Scratch& sc, int dtype, const void* A, int64_t lda, const vo
   const uint16_t* a_use = static_cast<const uint16_t*>(A);
   const uint16_t* b_use = static_cast<const uint16_t*>(B);
   if (!a_ok || !b_ok) {
-    // Unaligned rows: repack into zero-padded, 16-byte aligned copies.
+    // Operands that cannot be read in place: zero-padded, 16-byte aligned copies.
     uint16_t* a_p = static_cast<uint16_t*>(ws);
     uint16_t* b_p = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + a_sz);
     RepackJob ja{}, jb{};
