@@ -83,9 +83,14 @@ def _compile_torch_binding(verbose: bool) -> str:
     (host code only), and libhcg_gfx950.so found next to the module."""
     import torch.utils.cpp_extension as cpp
 
+    import torch
+
     tmp = TORCH_OUT + ".tmp"
+    # The C++ ABI the installed torch was built with (its headers' std::string
+    # layout must match ours).
+    abi = int(bool(torch._C._GLIBCXX_USE_CXX11_ABI))
     cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__",
-           "-DTORCH_EXTENSION_NAME=_hcg_torch", "-DTORCH_API_INCLUDE_EXTENSION_H", "-D_GLIBCXX_USE_CXX11_ABI=1",
+           "-DTORCH_EXTENSION_NAME=_hcg_torch", "-DTORCH_API_INCLUDE_EXTENSION_H", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
            *(f"-I{p}" for p in cpp.include_paths()), f"-I{sysconfig.get_paths()['include']}",
            "-I/opt/rocm/include", f"-I{INCLUDE}", TORCH_SRC, "-o", tmp,
            *(f"-L{p}" for p in cpp.library_paths()), "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",

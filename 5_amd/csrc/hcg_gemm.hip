@@ -2212,13 +2212,26 @@ bool chunk_tail_readable(const void* base, int64_t rows, int64_t cols, int64_t l
   const uintptr_t last = p + (uintptr_t)(((rows - 1) * ld + cols) * 2) - 1;
   const uintptr_t end = p + (uintptr_t)(((rows - 1) * ld + (int64_t)round_up(cols, 8)) * 2) + 16;
   if ((last >> 12) == ((end - 1) >> 12)) return true;
+  // The bytes past the last element reach one more page (at most 30 bytes
+  // are read past it).  It is readable when it lies inside the operand's
+  // allocation and is mapped: an address range reserved for virtual memory
+  // management can extend past what is mapped, so the page of the last byte
+  // read is also asked whether it is mapped (where the runtime cannot say,
+  // the allocation range decides).
   hipDeviceptr_t alloc = nullptr;
   size_t alloc_bytes = 0;
   if (hipMemGetAddressRange(&alloc, &alloc_bytes, const_cast<void*>(base)) != hipSuccess) {
     (void)hipGetLastError();  // not device memory of this process: stay on the safe side
     return false;
   }
-  return end <= reinterpret_cast<uintptr_t>(alloc) + alloc_bytes;
+  if (end > reinterpret_cast<uintptr_t>(alloc) + alloc_bytes) return false;
+  int mapped = 1;
+  if (hipPointerGetAttribute(&mapped, HIP_POINTER_ATTRIBUTE_MAPPED, static_cast<hipDeviceptr_t>(
+                                 reinterpret_cast<void*>(end - 1))) != hipSuccess) {
+    (void)hipGetLastError();
+    mapped = 1;
+  }
+  return mapped != 0;
 }
 
 // 16-bit operands: any element address is 2-byte aligned.
@@ -3094,5 +3107,17 @@ int hcg_gemm_noalloc(int dtype, const void* A, int64_t lda, const void* B, int64
 const char* hcg_last_error(void) { return t_last_error.c_str(); }
 
 int hcg_version(void) { return 100; }
+
+int hcg_operand_in_place(const void* base, int64_t rows, int64_t cols, int64_t ld) {
+  t_last_error.clear();
+  std::call_once(g_global_once, global_init);
+  if (base == nullptr || rows <= 0 || cols <= 0 || ld < cols) {
+    set_error(HCG_EINVAL, "operand: base %s, rows %lld, cols %lld, ld %lld", base ? "set" : "NULL",
+              (long long)rows, (long long)cols, (long long)ld);
+    return -1;
+  }
+  if (aligned16(base) && ld % 8 == 0) return 1;
+  return aligned2(base) && chunk_tail_readable(base, rows, cols, ld) ? 1 : 0;
+}
 
 }  // extern "C"

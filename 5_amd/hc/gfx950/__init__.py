@@ -292,7 +292,13 @@ def _fast_gemm() -> Any:
         _native.load()  # the library first: the binding links against it
         try:
             from . import _hcg_torch
-        except ImportError:
+        except ImportError as exc:
+            # Calls still run (through ctypes), at about 1.5 us more host
+            # time each; say so once rather than slow down silently.
+            import warnings
+
+            warnings.warn(f"hc.gfx950: the compiled device-tensor binding did not load ({exc}); "
+                          "calls on torch tensors go through ctypes", RuntimeWarning, stacklevel=3)
             _FAST = False
         else:
             _FAST = _hcg_torch.gemm

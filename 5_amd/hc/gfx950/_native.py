@@ -12,7 +12,6 @@ dynamic loader reuses an already-loaded SONAME.
 from __future__ import annotations
 
 import ctypes
-import gc
 import os
 import threading
 
@@ -54,7 +53,7 @@ ALGOS = {
 
 # Every symbol include/hcg_gemm.h and include/hcg_tile_ops.h declare.
 EXPORTS = ("hcg_init", "hcg_gemm", "hcg_gemm_algo", "hcg_gemm_noalloc", "hcg_last_error", "hcg_version",
-           "hcg_tile_load", "hcg_tile_store")
+           "hcg_operand_in_place", "hcg_tile_load", "hcg_tile_store")
 
 NOALLOC_SCRATCH_BYTES = 32 << 20  # HCG_NOALLOC_SCRATCH_BYTES
 
@@ -78,6 +77,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.hcg_last_error.restype = ctypes.c_char_p
     lib.hcg_version.argtypes = []
     lib.hcg_version.restype = c_int
+    lib.hcg_operand_in_place.argtypes = [vp, i64, i64, i64]
+    lib.hcg_operand_in_place.restype = c_int
     u64 = ctypes.c_uint64
     lib.hcg_tile_load.argtypes = [c_int, vp, i64, i64, i64, vp, i64, i64, i64, vp, u64, vp, vp, vp]
     lib.hcg_tile_load.restype = c_int
@@ -104,15 +105,11 @@ def load() -> ctypes.CDLL:
         except OSError as exc:
             raise BackendError(f"cannot load {LIB_PATH}: {exc}") from exc
         _declare(lib)
-        # The process's first full (generation 2) garbage collection after
-        # torch is imported scans ~170k objects and holds the interpreter for
-        # 40-50 ms; left alone, the few objects each call allocates trigger
-        # it a few hundred launches in, and the GPU idles while the host is
-        # stopped.  Freezing the objects that exist now (the imported modules
-        # and their data, which live for the whole process) takes them out
-        # of every later collection, so no collection ever rescans them; a
-        # collection here instead would cost those 40-50 ms on the first call.
-        gc.freeze()
+        # Loading leaves the process's garbage collector as it was.  (Its
+        # first full collection after torch is imported scans ~170k objects
+        # and stops the host for 40-50 ms a few hundred calls in; a caller
+        # that minds runs gc.collect() and gc.freeze() once after its imports,
+        # as bench.py does.)
         _lib = lib
         return lib
 

@@ -108,6 +108,17 @@ const char* hcg_last_error(void);
 /* ABI version of this library (major * 100 + minor). */
 int hcg_version(void);
 
+/* Whether the DMA kernels read a 16-bit rows x cols operand at `base` (row
+ * stride ld elements) in place: 1 in place, 0 copied first into zero-padded
+ * rows, -1 for bad arguments (text in hcg_last_error()).  Rows that are 16-byte
+ * aligned are read in place; other rows are read in 16-byte pieces, which
+ * reach up to 30 bytes past the last element, so they are read in place only
+ * when those bytes lie in the last element's 4 KB page, or inside the
+ * operand's device allocation and mapped.  Queries the HIP runtime about the
+ * pointer and launches nothing.  No counterpart in the reference (which has
+ * no device memory); for tests and diagnostics. */
+int hcg_operand_in_place(const void* base, int64_t rows, int64_t cols, int64_t ld);
+
 #ifdef __cplusplus
 }
 #endif

@@ -117,3 +117,42 @@ def test_device_tensor_binding_is_built_and_leaves_other_cases_to_python():
 
     a = torch.zeros((4, 4), dtype=torch.float16)
     assert _hcg_torch.gemm(a, a, torch.zeros((4, 4)), 0) == -1
+
+
+def test_loading_the_library_leaves_the_garbage_collector_alone():
+    """Opening the library (and importing the package) neither freezes nor
+    disables Python's cyclic garbage collector: that stays the caller's
+    choice.  Runs in a fresh interpreter, where nothing has loaded it yet."""
+    import subprocess
+    import sys
+
+    code = (
+        "import gc, sys; sys.path[:0] = [%r];"
+        "before = (gc.get_freeze_count(), gc.isenabled(), gc.get_threshold());"
+        "import hc, hc.gfx950; from hc.gfx950 import _native; _native.load();"
+        "after = (gc.get_freeze_count(), gc.isenabled(), gc.get_threshold());"
+        "assert before == after, (before, after); print('ok')"
+    ) % os.path.join(ROOT, "5_amd")
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0 and out.stdout.strip() == "ok", out.stderr
+
+
+def test_operand_query_without_device_memory():
+    """hcg_operand_in_place decides on the host.  Rows 16-byte aligned: in
+    place; an odd address: copied; a tail whose extra bytes stay in the last
+    element's 4 KB page: in place without asking the runtime; a tail that
+    crosses into the next page of memory the runtime does not know (here host
+    memory): copied."""
+    lib = _native.load()
+    q = lib.hcg_operand_in_place
+    assert q(0x10000, 4, 8, 8) == 1  # aligned rows
+    assert q(0x10001, 1, 3, 3) == 0  # odd address
+    # 1 x 3 at 0x10002: last byte 0x10007, the 16-byte pieces read to 0x10021
+    assert q(0x10002, 1, 3, 3) == 1
+    # rows at 2-byte alignment ending 2 bytes before a page boundary: the
+    # pieces read past it, into a page the runtime knows nothing about
+    buf = ctypes.create_string_buffer(3 * 4096)
+    page = (ctypes.addressof(buf) + 4095) & ~4095
+    assert q(page + 4096 - 2 * 11 - 2, 1, 11, 11) == 0
+    assert q(None, 1, 1, 1) == -1 and "NULL" in _native.last_error(lib)
+    assert q(0x10000, 2, 8, 7) == -1 and "ld 7" in _native.last_error(lib)
