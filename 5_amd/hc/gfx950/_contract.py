@@ -34,9 +34,13 @@ when the kernel *is* that GEMM, so a kernel is accepted only after two checks:
    fallback body, the verify hook) and must also carry a lowering registered
    for an ``amdgpu-*`` target -- ``mfma_gfx950``'s ``amdgpu-gfx950`` lowering
    or the reference's ``wmma_gfx11`` ``amdgpu-gfx11`` one; the GPU kernel
-   replaces the whole loop of them.  The inputs are small integers, so every
+   replaces the whole loop of them.  The inputs are integers, so every
    summation order is exact and C must equal A @ B exactly; an element left
-   unwritten (C starts as NaN) or any other value rejects the kernel.
+   unwritten (C starts as NaN) or any other value rejects the kernel.  Two
+   runs are made: one with small values, and one whose partial sums reach
+   ~10^6, which only float32 accumulation computes exactly (the reference
+   folds in np.float32, examples/amdgpu_gfx11_wmma_matmul.py:183-190); the
+   accumulator the init and accumulate helpers return must be float32.
 
 A kernel that fails either check raises ``LaunchError`` naming it and the
 reason.  Results are cached per kernel function.  The check runs the
@@ -207,8 +211,9 @@ def _function_node(fn: Any) -> ast.FunctionDef:
     return node
 
 
-def _check_structure(fn: Any, a: str, b: str, c: str) -> tuple[int, int, int]:
-    """Checks the body's statements; returns (TM, TN, TK)."""
+def _check_structure(fn: Any, a: str, b: str, c: str) -> tuple[tuple[int, int, int], tuple[Any, Any]]:
+    """Checks the body's statements; returns (TM, TN, TK) and the init and
+    accumulate helpers."""
     node = _function_node(fn)
     params = [arg.arg for arg in node.args.args]
     if node.args.vararg or node.args.kwarg or node.args.kwonlyargs or node.args.posonlyargs:
@@ -248,7 +253,7 @@ def _check_structure(fn: Any, a: str, b: str, c: str) -> tuple[int, int, int]:
         raise _Reject("the second statement must initialise the accumulator")
     acc = _name(init.targets[0])
     init_call = _plain_call(init.value)
-    _helper(init_call.func, env, "accumulator init")
+    init_helper = _helper(init_call.func, env, "accumulator init")
     if not _args_are(init_call, (group,)):
         raise _Reject("the accumulator init must take only the group")
 
@@ -294,7 +299,7 @@ def _check_structure(fn: Any, a: str, b: str, c: str) -> tuple[int, int, int]:
     if not (isinstance(accumulate, ast.Assign) and len(accumulate.targets) == 1 and _name(accumulate.targets[0]) == acc):
         raise _Reject(f"the K loop must end with {acc} = <accumulate>(group, a_tile, b_tile, {acc})")
     acc_call = _plain_call(accumulate.value)
-    _helper(acc_call.func, env, "accumulate step")
+    acc_helper = _helper(acc_call.func, env, "accumulate step")
     if not _args_are(acc_call, (group, ta, tb, acc)):
         raise _Reject(f"the accumulate step must take ({group}, {ta}, {tb}, {acc})")
     if len({row0, col0, acc, k, ta, tb, group, a, b, c}) != 10:
@@ -307,7 +312,7 @@ def _check_structure(fn: Any, a: str, b: str, c: str) -> tuple[int, int, int]:
     _helper(store_call.func, env, "store")
     if not _args_are(store_call, (group, c, row0, col0, acc)):
         raise _Reject(f"the store must take ({group}, {c}, {row0}, {col0}, {acc})")
-    return tm, tn, step
+    return (tm, tn, step), (env[init_helper], env[acc_helper])
 
 
 # --------------------------------------------------------------------------
@@ -599,6 +604,7 @@ class _Run:
         self.intrinsics: set[str] = set()
         self.error: str | None = None
         self.codes: dict[Any, Any] = {}  # code object -> hc helper / intrinsic, or None
+        self.acc_codes: dict[Any, str] = {}  # code object of the init / accumulate helper -> its name
 
     def require_group_scope(self, what: str) -> None:
         if self.scope is not WorkGroup:
@@ -616,6 +622,15 @@ class _Run:
         elif declared is not self.scope:
             self.fail(f"{kind} {fn.__name__!r} runs in {self.scope.__name__ if self.scope is WorkItem else 'WorkGroup'} "
                       f"scope but declares {declared.__name__ if declared is WorkItem else 'WorkGroup'}")
+
+    def on_accumulator(self, name: str, value: Any) -> None:
+        """The kernel's accumulator must be float32, as the reference's is
+        (examples/amdgpu_gfx11_wmma_matmul.py:183-190 folds in np.float32):
+        the GPU kernels accumulate in float32 whatever the helpers do."""
+        if not isinstance(value, _Masked):
+            self.fail(f"helper {name!r} returns {type(value).__name__}, not a float32 accumulator")
+        elif value.dtype != np.dtype(np.float32):
+            self.fail(f"helper {name!r} returns a {value.dtype} accumulator, not float32")
 
     def on_intrinsic(self, fn: Any, frame: Any) -> None:
         self.check_scope("intrinsic", fn, fn.__hc_intrinsic__.scope)
@@ -652,6 +667,13 @@ class _Run:
 
 
 def _profile(frame: Any, event: str, arg: Any) -> None:
+    if event == "return":
+        run = getattr(_ACTIVE, "run", None)
+        if run is not None:
+            name = run.acc_codes.get(frame.f_code)
+            if name is not None:
+                run.on_accumulator(name, arg)
+        return
     if event != "call":
         return
     run = getattr(_ACTIVE, "run", None)
@@ -677,20 +699,34 @@ def _profile(frame: Any, event: str, arg: Any) -> None:
 _UNSEEN = object()
 
 
-def _probe_inputs(tm: int, tn: int, tk: int, dtype: str) -> tuple[np.ndarray, np.ndarray]:
+# The recorded runs' input ranges.  Every value is an integer the element
+# type holds exactly (float16 up to 2048, bfloat16 up to 256) and every
+# partial sum stays below 2^24, so float32 accumulation in any order gives
+# A @ B exactly.  The first probe's sums stay small (a kernel that is not the
+# contraction fails it whatever its arithmetic); the second's reach ~10^6, so
+# accumulating in float16 or bfloat16, or clamping, gives other values.
+_PROBES = ("small", "wide")
+
+
+def _probe_inputs(tm: int, tn: int, tk: int, dtype: str, probe: str) -> tuple[np.ndarray, np.ndarray]:
     m, n, k = tm + tm // 2 + 1, tn + tn // 2 + 1, tk + tk // 2 + 1
-    rng = np.random.default_rng(0x5EED)
-    # Small integers: exact in float16 and bfloat16 and in any float32
-    # summation order.  bfloat16 kernels see them as float32 payloads.
+    rng = np.random.default_rng(0x5EED if probe == "small" else 0x5EED + 1)
+    # bfloat16 kernels see their values as float32 payloads.
     payload = np.float16 if dtype == "float16" else np.float32
-    a = rng.integers(-3, 4, size=(m, k)).astype(payload)
-    b = rng.integers(-3, 4, size=(k, n)).astype(payload)
+    if probe == "small":
+        lo = 3
+    else:
+        lo = 200 if dtype == "float16" else 128
+        lo = min(lo, int(np.sqrt((1 << 24) / (2 * k))))
+    a = rng.integers(-lo, lo + 1, size=(m, k)).astype(payload)
+    b = rng.integers(-lo, lo + 1, size=(k, n)).astype(payload)
     return a, b
 
 
-def _record(fn: Any, names: tuple[str, str, str], tile: tuple[int, int, int], dtype: str, target: Any) -> tuple[str, ...]:
+def _record(fn: Any, names: tuple[str, str, str], tile: tuple[int, int, int], dtype: str, target: Any,
+            helpers: tuple[Any, Any], probe: str) -> tuple[str, ...]:
     a_name, b_name, c_name = names
-    a, b = _probe_inputs(*tile, dtype)
+    a, b = _probe_inputs(*tile, dtype, probe)
     m, k = a.shape
     n = b.shape[1]
     c = np.full((m, n), np.nan, dtype=np.float32)
@@ -699,6 +735,8 @@ def _record(fn: Any, names: tuple[str, str, str], tile: tuple[int, int, int], dt
     if any(d == 0 for d in counts):
         raise _Reject("its launch geometry is empty for a non-empty problem")
     run = _Run(geometry.env, target)
+    for helper in helpers:
+        run.acc_codes[helper.__code__] = helper.__name__
     params = list(inspect.signature(fn).parameters)[1:]
     buffers = {a_name: a, b_name: b, c_name: c}
     previous = sys.getprofile()
@@ -726,7 +764,8 @@ def _record(fn: Any, names: tuple[str, str, str], tile: tuple[int, int, int], dt
         raise _Reject(f"a {m}x{n}x{k} probe leaves {missing} elements of {c_name} unwritten")
     wrong = int((c != want).sum())
     if wrong:
-        raise _Reject(f"a {m}x{n}x{k} probe computes {wrong} elements of {c_name} that differ from A @ B")
+        what = "" if probe == "small" else " with partial sums that need float32 accumulation"
+        raise _Reject(f"a {m}x{n}x{k} probe{what} computes {wrong} elements of {c_name} that differ from A @ B")
     return tuple(sorted(run.intrinsics))
 
 
@@ -758,8 +797,10 @@ def _recognise(fn: Any, target: Any) -> Contraction:
         raise _Reject("its buffers are not (Buffer[M, K, T], Buffer[K, N, T], Buffer[M, N, float32]) with T "
                       "float16 or bfloat16")
     a, b, c, dtype = sig
-    tile = _check_structure(fn, a, b, c)
-    intrinsics = _record(fn, (a, b, c), tile, dtype, target)
+    tile, helpers = _check_structure(fn, a, b, c)
+    intrinsics: tuple[str, ...] = ()
+    for probe in _PROBES:
+        intrinsics = _record(fn, (a, b, c), tile, dtype, target, helpers, probe)
     return Contraction(a=a, b=b, c=c, dtype=dtype, tile=tile, intrinsics=intrinsics)
 
 

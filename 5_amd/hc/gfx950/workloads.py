@@ -66,9 +66,12 @@ CONFIGS: dict[str, GemmConfig] = {
 
 
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
-    """float32 -> bfloat16 bits, round to nearest even (finite inputs)."""
-    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    """float32 -> bfloat16 bits, round to nearest even (finite inputs).
+
+    In uint32: a finite float32's bits are at most 0xFF7FFFFF, so adding at
+    most 0x8000 cannot wrap."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    return ((u + (0x7FFF + ((u >> 16) & 1))) >> 16).astype(np.uint16)
 
 
 def _draw(rng: np.random.Generator, dist: tuple[str, float], shape: tuple[int, int]) -> np.ndarray:

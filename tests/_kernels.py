@@ -317,3 +317,141 @@ def some_other_kernel(
 def tiled_gfx950_mfma_matmul(group, x: Buffer[M, np.float16]) -> None:
     """The package kernel's name, but not a contraction signature."""
     raise AssertionError("never runs")
+
+
+# Near misses in the arithmetic: the same structure, with intrinsics whose
+# fallback bodies accumulate more narrowly than float32.  On small integer
+# inputs they agree with A @ B; the launch must still reject them, because
+# the GPU kernel would accumulate in float32 and return other results than
+# the simulator gives for them.
+
+
+def _narrow_fold(a_tile, b_tile, acc_frag, lane, wave_size, fold_type, clamp, out_type):
+    a_tile = a_tile.with_inactive(value=np.float16(0))
+    b_tile = b_tile.with_inactive(value=np.float16(0))
+    rows = lane_rows(lane, wave_size)
+    out = np.empty((len(rows),), dtype=out_type)
+    with np.errstate(over="ignore"):  # float16 sums overflow on the wide probe
+        for i, row in enumerate(rows):
+            s = fold_type(acc_frag[i])
+            for kk in range(TILE):
+                s = fold_type(s + fold_type(a_tile[row, kk]) * fold_type(b_tile[kk, lane % TILE]))
+            out[i] = min(max(s, -clamp), clamp) if clamp else s
+    return out
+
+
+def _lower_as_wmma(ctx, group, a_tile, b_tile, a_frag, b_frag, acc_frag, *, lane, wave_size, arch):
+    return _lower_wmma(ctx, group, a_tile, b_tile, a_frag, b_frag, acc_frag, lane=lane, wave_size=wave_size,
+                       arch=arch)
+
+
+@kernel.intrinsic(scope=WorkItem, effects="pure", const_attrs={"wave_size", "arch"},
+                  result_types=(vector_type((ROWS_PER_LANE,), np.float32),))
+def wmma_f16_fold(group, a_tile, b_tile, a_frag, b_frag, acc_frag, *, lane, wave_size, arch):
+    """Sums in float16, returns float32."""
+    _ = (a_frag, b_frag, arch)
+    out = _narrow_fold(a_tile, b_tile, acc_frag, lane, wave_size, np.float16, None, np.float32)
+    return group.vload(out, shape=(len(out),))
+
+
+@kernel.intrinsic(scope=WorkItem, effects="pure", const_attrs={"wave_size", "arch"},
+                  result_types=(vector_type((ROWS_PER_LANE,), np.float32),))
+def wmma_clamped(group, a_tile, b_tile, a_frag, b_frag, acc_frag, *, lane, wave_size, arch):
+    """Sums in float32, clamps each result to [-4096, 4096]."""
+    _ = (a_frag, b_frag, arch)
+    out = _narrow_fold(a_tile, b_tile, acc_frag, lane, wave_size, np.float32, np.float32(4096), np.float32)
+    return group.vload(out, shape=(len(out),))
+
+
+@kernel.intrinsic(scope=WorkItem, effects="pure", const_attrs={"wave_size", "arch"},
+                  result_types=(vector_type((ROWS_PER_LANE,), np.float16),))
+def wmma_f16_result(group, a_tile, b_tile, a_frag, b_frag, acc_frag, *, lane, wave_size, arch):
+    """Sums in float32, returns the accumulator rounded to float16."""
+    _ = (a_frag, b_frag, arch)
+    out = _narrow_fold(a_tile, b_tile, acc_frag, lane, wave_size, np.float32, None, np.float16)
+    return group.vload(out, shape=(len(out),))
+
+
+for _narrow in (wmma_f16_fold, wmma_clamped, wmma_f16_result):
+    _narrow.lower(target="amdgpu-gfx11")(_lower_as_wmma)
+
+
+@kernel.func(scope=WorkGroup)
+def f16_fold_step(group, a_tile, b_tile, acc):
+    @group.workitems
+    def lanes(wi):
+        lane = wi.local_id()[0]
+        return wmma_f16_fold(group, a_tile, b_tile, a_fragment(wi, a_tile), b_fragment(wi, b_tile),
+                             acc[:, lane, 0], lane=lane, wave_size=LANES, arch="gfx11")
+
+    return lanes()
+
+
+@kernel.func(scope=WorkGroup)
+def clamped_step(group, a_tile, b_tile, acc):
+    @group.workitems
+    def lanes(wi):
+        lane = wi.local_id()[0]
+        return wmma_clamped(group, a_tile, b_tile, a_fragment(wi, a_tile), b_fragment(wi, b_tile),
+                            acc[:, lane, 0], lane=lane, wave_size=LANES, arch="gfx11")
+
+    return lanes()
+
+
+@kernel.func(scope=WorkGroup)
+def f16_result_step(group, a_tile, b_tile, acc):
+    @group.workitems
+    def lanes(wi):
+        lane = wi.local_id()[0]
+        return wmma_f16_result(group, a_tile, b_tile, a_fragment(wi, a_tile), b_fragment(wi, b_tile),
+                               acc[:, lane, 0], lane=lane, wave_size=LANES, arch="gfx11")
+
+    return lanes()
+
+
+@kernel(**GEOMETRY)
+def f16_fold_kernel(
+    group,
+    a: Buffer[M, K, np.float16],
+    b: Buffer[K, N, np.float16],
+    c: Buffer[M, N, np.float32],
+) -> None:
+    row0, col0 = tile_origin(group.group_id[0], group.group_id[1])
+    acc = zero_acc(group)
+    for k0 in range(0, a.shape[1], TILE):
+        a_tile = group.load(a[row0 : row0 + TILE, k0 : k0 + TILE], shape=(TILE, TILE))
+        b_tile = group.load(b[k0 : k0 + TILE, col0 : col0 + TILE], shape=(TILE, TILE))
+        acc = f16_fold_step(group, a_tile, b_tile, acc)
+    store_acc(group, c, row0, col0, acc)
+
+
+@kernel(**GEOMETRY)
+def clamped_kernel(
+    group,
+    a: Buffer[M, K, np.float16],
+    b: Buffer[K, N, np.float16],
+    c: Buffer[M, N, np.float32],
+) -> None:
+    row0, col0 = tile_origin(group.group_id[0], group.group_id[1])
+    acc = zero_acc(group)
+    for k0 in range(0, a.shape[1], TILE):
+        a_tile = group.load(a[row0 : row0 + TILE, k0 : k0 + TILE], shape=(TILE, TILE))
+        b_tile = group.load(b[k0 : k0 + TILE, col0 : col0 + TILE], shape=(TILE, TILE))
+        acc = clamped_step(group, a_tile, b_tile, acc)
+    store_acc(group, c, row0, col0, acc)
+
+
+@kernel(**GEOMETRY)
+def f16_result_kernel(
+    group,
+    a: Buffer[M, K, np.float16],
+    b: Buffer[K, N, np.float16],
+    c: Buffer[M, N, np.float32],
+) -> None:
+    row0, col0 = tile_origin(group.group_id[0], group.group_id[1])
+    acc = zero_acc(group)
+    for k0 in range(0, a.shape[1], TILE):
+        a_tile = group.load(a[row0 : row0 + TILE, k0 : k0 + TILE], shape=(TILE, TILE))
+        b_tile = group.load(b[k0 : k0 + TILE, col0 : col0 + TILE], shape=(TILE, TILE))
+        acc = f16_result_step(group, a_tile, b_tile, acc)
+    store_acc(group, c, row0, col0, acc)

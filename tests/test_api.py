@@ -173,6 +173,9 @@ def test_the_package_kernels_are_recognised_through_their_mfma_intrinsic():
         ("half_grid_kernel", r"leaves \d+ elements of c unwritten"),
         ("unlowered_kernel", "has no lowering registered for an amdgpu target"),
         ("some_other_kernel", "the body must be"),
+        ("f16_fold_kernel", r"probe with partial sums that need float32 accumulation computes \d+ elements"),
+        ("clamped_kernel", r"probe with partial sums that need float32 accumulation computes \d+ elements"),
+        ("f16_result_kernel", "helper 'f16_result_step' returns a float16 accumulator, not float32"),
     ],
 )
 def test_near_misses_are_rejected_with_the_reason(name, reason):

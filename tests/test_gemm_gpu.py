@@ -173,7 +173,7 @@ def test_compiled_handle_launches():
 # -- BASELINE.json configurations ------------------------------------------------
 
 
-@pytest.mark.parametrize("name", ["c1_128_f16", "c2_4096_f16", "c4_skinny_f16", "c5_ragged_f16"])
+@pytest.mark.parametrize("name", ["c1_128_f16", "c2_4096_f16", "c3_8192_bf16", "c4_skinny_f16", "c5_ragged_f16"])
 def test_baseline_config_full_size_against_oracle(name):
     from hc.gfx950.workloads import CONFIGS, make_inputs
 
@@ -185,17 +185,16 @@ def test_baseline_config_full_size_against_oracle(name):
     _check(got, want, cfg.k)
 
 
-def test_c3_bf16_8192_sampled_rows_and_checksums():
+def test_c3_bf16_8192_row_sums():
+    """A size-independent property over the whole C3 output besides the
+    elementwise check above: row sums of C equal A @ (B @ 1) (float64 on the
+    host)."""
     from hc.gfx950.workloads import CONFIGS, make_inputs
 
     cfg = CONFIGS["c3_8192_bf16"]
-    print("case c3 8192^3 bf16", flush=True)
+    print("case c3 8192^3 bf16 row sums", flush=True)
     a, b = make_inputs(cfg, seed=0)
     got = _gemm(a, b, dtype=cfg.dtype)
-    rows = np.arange(0, cfg.m, 61, dtype=np.int64)
-    _check(got[rows], oracle.gemm_c_rows(a, b, rows, oracle.BF16), cfg.k)
-    # Size-independent property over the whole output: row sums of C equal
-    # A @ (B @ 1) (float64 on the host).
     a64 = oracle.bf16_bits_to_f32(a).astype(np.float64)
     b64 = oracle.bf16_bits_to_f32(b).astype(np.float64)
     want = a64 @ b64.sum(axis=1)

@@ -62,11 +62,18 @@ def test_bf16_rounding_matches_torch():
             rng.normal(0, 0.02, 20000).astype(np.float32),
             # exact ties: low 16 bits 0x8000, even and odd kept parts
             (np.array([0x3F808000, 0x3F818000, 0xBF808000, 0x00008000], dtype=np.uint32)).view(np.float32),
+            # the largest finite magnitudes (the rounding add must not wrap;
+            # 0x7F7F8000 and up round to infinity, as torch does), subnormals
+            (np.array([0x7F7FFFFF, 0xFF7FFFFF, 0x7F7F7FFF, 0xFF7F8000, 0x00000001, 0x807FFFFF],
+                      dtype=np.uint32)).view(np.float32),
         ]
     )
     ours = oracle.f32_to_bf16_bits(x)
     theirs = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(ours, theirs)
+    from hc.gfx950.workloads import f32_to_bf16_bits
+
+    assert np.array_equal(f32_to_bf16_bits(x), theirs)
 
 
 def test_bf16_tie_cases_by_hand():
