@@ -2,8 +2,9 @@
 
     python 5_amd/csrc/build.py [-v]
 
-compiles 5_amd/csrc/hcg_gemm.hip and hcg_tile.hip (kernels + the C ABI
-declared in include/hcg_gemm.h and include/hcg_tile_ops.h) with hipcc for
+compiles 5_amd/csrc/hcg_gemm.hip, hcg_tile.hip and hcg_mfma.hip (kernels +
+the C ABI declared in include/hcg_gemm.h, include/hcg_tile_ops.h and
+include/hcg_mfma.h) with hipcc for
 gfx950 into
 5_amd/hc/gfx950/libhcg_gfx950.so, next to the Python code that loads it,
 and hcg_probe.hip (the hardware ceiling probes of include/hcg_probe.h, used
@@ -25,7 +26,7 @@ import sysconfig
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
-SRCS = [os.path.join(HERE, "hcg_gemm.hip"), os.path.join(HERE, "hcg_tile.hip")]
+SRCS = [os.path.join(HERE, f) for f in ("hcg_gemm.hip", "hcg_tile.hip", "hcg_mfma.hip")]
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(PKG, "hc", "gfx950", "libhcg_gfx950.so")
 PROBE_SRCS = [os.path.join(HERE, "hcg_probe.hip")]

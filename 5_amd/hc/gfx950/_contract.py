@@ -32,9 +32,16 @@ when the kernel *is* that GEMM, so a kernel is accepted only after two checks:
    an inactive element is an error).  Each call of an intrinsic is checked
    as the simulator checks it (hc/simulator.py:972-1001: declared scope, a
    fallback body, the verify hook) and must also carry a lowering registered
-   for an ``amdgpu-*`` target -- ``mfma_gfx950``'s ``amdgpu-gfx950`` lowering
-   or the reference's ``wmma_gfx11`` ``amdgpu-gfx11`` one; the GPU kernel
-   replaces the whole loop of them.  The inputs are integers, so every
+   for ``amdgpu-gfx950`` (``mfma_gfx950``, ``mfma16_gfx950``) or
+   ``amdgpu-gfx11`` (the reference's ``wmma_gfx11``).  That lowering callback
+   is called, once per call site, with a recording ``ctx`` (``_lowering``):
+   the op it creates must be a matrix-core instruction this library executes
+   (``rocdl.mfma.f32.32x32x16`` / ``16x16x32``, or the reference's
+   ``amdgpu.wmma``), with matching ``m``/``n``/``k``/``arch``/``wave_size``,
+   a float32 vector result and the accumulator as its last operand, and its
+   m x n x k must be the kernel's tile and K step (one op per lane and K
+   step computes the tile) for waves of the workgroup's size.  The GPU
+   kernel replaces the whole loop of them.  The inputs are integers, so every
    summation order is exact and C must equal A @ B exactly; an element left
    unwritten (C starts as NaN) or any other value rejects the kernel.  Two
    runs are made: one with small values, and one whose partial sums reach
@@ -63,6 +70,7 @@ import numpy as np
 
 from .._errors import LaunchError
 from .._launch import launch_geometry, resolved_annotations
+from ._lowering import TARGET_ARCH, TARGET_ORDER, Location, LoweringError, check_matrix_op, lowering_target, record_lowering
 from ..core import BufferSpec, WorkGroup, WorkItem
 from ..symbols import Expr, Symbol
 
@@ -80,6 +88,7 @@ class Contraction:
     dtype: str  # "float16" or "bfloat16"
     tile: tuple[int, int, int]  # (TM, TN, TK) of one workgroup's tile and K step
     intrinsics: tuple[str, ...]  # intrinsics the recorded run called
+    ops: tuple[str, ...] = ()  # the ops their lowerings create (recorded through a ctx)
 
 
 class _Reject(Exception):
@@ -605,6 +614,8 @@ class _Run:
         self.error: str | None = None
         self.codes: dict[Any, Any] = {}  # code object -> hc helper / intrinsic, or None
         self.acc_codes: dict[Any, str] = {}  # code object of the init / accumulate helper -> its name
+        # intrinsic call site -> (lowered op, its (m, n, k), its wave size)
+        self.lowered: dict[Any, tuple[str, tuple[int, int, int], int]] = {}
 
     def require_group_scope(self, what: str) -> None:
         if self.scope is not WorkGroup:
@@ -640,30 +651,50 @@ class _Run:
         lowerings = getattr(fn, "__hc_lowerings__", {}) or {}
         if not any(str(t).startswith("amdgpu-") for t in lowerings):
             self.fail(f"intrinsic {fn.__name__!r} has no lowering registered for an amdgpu target")
+            return
+        target = lowering_target(fn)
+        if target is None:
+            self.fail(f"intrinsic {fn.__name__!r} has lowerings for {', '.join(sorted(map(str, lowerings)))}, "
+                      f"none of which this library executes ({', '.join(TARGET_ORDER)})")
+            return
         self.intrinsic_calls += 1
         self.intrinsics.add(fn.__name__)
+        args: list[Any] = []
+        kwargs: dict[str, Any] = {}
+        local = frame.f_locals
+        for param in inspect.signature(fn).parameters.values():
+            if param.kind in (param.POSITIONAL_ONLY, param.POSITIONAL_OR_KEYWORD):
+                args.append(local[param.name])
+            elif param.kind is param.VAR_POSITIONAL:
+                args.extend(local.get(param.name, ()))
+            elif param.kind is param.KEYWORD_ONLY:
+                kwargs[param.name] = local[param.name]
+            else:
+                kwargs.update(local.get(param.name, {}))
         verify = getattr(fn, "__hc_verify__", None)
-        if verify is None:
+        if verify is not None:
+            try:
+                result = verify(_CallSig(self.scope, tuple(args), kwargs), self.target)
+            except Exception as exc:  # noqa: BLE001 - the hook's failure is the verdict
+                self.fail(f"intrinsic {fn.__name__!r} verify hook failed: {exc}")
+                return
+            if result is False:
+                self.fail(f"intrinsic {fn.__name__!r} verify hook returned False")
+                return
+        # The lowering replaces this call on its target: call it as the
+        # compiler would and check the op it creates (once per call site).
+        caller = frame.f_back
+        site = (fn, caller.f_code, caller.f_lineno) if caller is not None else (fn, None, 0)
+        if site in self.lowered:
             return
+        loc = Location(caller.f_code.co_filename, caller.f_lineno) if caller is not None else None
         try:
-            args: list[Any] = []
-            kwargs: dict[str, Any] = {}
-            local = frame.f_locals
-            for param in inspect.signature(fn).parameters.values():
-                if param.kind in (param.POSITIONAL_ONLY, param.POSITIONAL_OR_KEYWORD):
-                    args.append(local[param.name])
-                elif param.kind is param.VAR_POSITIONAL:
-                    args.extend(local.get(param.name, ()))
-                elif param.kind is param.KEYWORD_ONLY:
-                    kwargs[param.name] = local[param.name]
-                else:
-                    kwargs.update(local.get(param.name, {}))
-            result = verify(_CallSig(self.scope, tuple(args), kwargs), self.target)
-        except Exception as exc:  # noqa: BLE001 - the hook's failure is the verdict
-            self.fail(f"intrinsic {fn.__name__!r} verify hook failed: {exc}")
+            op = record_lowering(fn, target, tuple(args), kwargs, loc)
+            shape = check_matrix_op(op, target, fn, tuple(args))
+        except LoweringError as exc:
+            self.fail(str(exc))
             return
-        if result is False:
-            self.fail(f"intrinsic {fn.__name__!r} verify hook returned False")
+        self.lowered[site] = (op.name, shape, TARGET_ARCH[target][1])
 
 
 def _profile(frame: Any, event: str, arg: Any) -> None:
@@ -724,7 +755,7 @@ def _probe_inputs(tm: int, tn: int, tk: int, dtype: str, probe: str) -> tuple[np
 
 
 def _record(fn: Any, names: tuple[str, str, str], tile: tuple[int, int, int], dtype: str, target: Any,
-            helpers: tuple[Any, Any], probe: str) -> tuple[str, ...]:
+            helpers: tuple[Any, Any], probe: str) -> tuple[tuple[str, ...], tuple[str, ...]]:
     a_name, b_name, c_name = names
     a, b = _probe_inputs(*tile, dtype, probe)
     m, k = a.shape
@@ -758,6 +789,16 @@ def _record(fn: Any, names: tuple[str, str, str], tile: tuple[int, int, int], dt
         raise _Reject(run.error)
     if run.intrinsic_calls == 0:
         raise _Reject("its accumulate step calls no intrinsic")
+    lanes = int(np.prod(geometry.group_shape))
+    for op_name, shape, wave in run.lowered.values():
+        # One lowered op per lane and K step computes the whole workgroup
+        # tile, as the GPU kernels' matrix-core steps do.
+        if shape != tile:
+            raise _Reject(f"its intrinsic lowers to {op_name} (m x n x k = {shape[0]} x {shape[1]} x {shape[2]}), "
+                          f"which does not compute its {tile[0]} x {tile[1]} tile over a K step of {tile[2]}")
+        if wave != lanes:
+            raise _Reject(f"its intrinsic lowers to {op_name} for {wave}-lane waves, but a workgroup has {lanes} "
+                          "workitems")
     want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
     missing = int(np.isnan(c).sum())
     if missing:
@@ -766,7 +807,7 @@ def _record(fn: Any, names: tuple[str, str, str], tile: tuple[int, int, int], dt
     if wrong:
         what = "" if probe == "small" else " with partial sums that need float32 accumulation"
         raise _Reject(f"a {m}x{n}x{k} probe{what} computes {wrong} elements of {c_name} that differ from A @ B")
-    return tuple(sorted(run.intrinsics))
+    return tuple(sorted(run.intrinsics)), tuple(sorted({name for name, _, _ in run.lowered.values()}))
 
 
 _CACHE: dict[Any, Contraction | str] = {}
@@ -799,9 +840,10 @@ def _recognise(fn: Any, target: Any) -> Contraction:
     a, b, c, dtype = sig
     tile, helpers = _check_structure(fn, a, b, c)
     intrinsics: tuple[str, ...] = ()
+    ops: tuple[str, ...] = ()
     for probe in _PROBES:
-        intrinsics = _record(fn, (a, b, c), tile, dtype, target, helpers, probe)
-    return Contraction(a=a, b=b, c=c, dtype=dtype, tile=tile, intrinsics=intrinsics)
+        intrinsics, ops = _record(fn, (a, b, c), tile, dtype, target, helpers, probe)
+    return Contraction(a=a, b=b, c=c, dtype=dtype, tile=tile, intrinsics=intrinsics, ops=ops)
 
 
 def forget(fn: Any) -> None:

@@ -51,9 +51,9 @@ ALGOS = {
     "narrow": HCG_ALGO_NARROW,
 }
 
-# Every symbol include/hcg_gemm.h and include/hcg_tile_ops.h declare.
+# Every symbol include/hcg_gemm.h, include/hcg_tile_ops.h and include/hcg_mfma.h declare.
 EXPORTS = ("hcg_init", "hcg_gemm", "hcg_gemm_algo", "hcg_gemm_noalloc", "hcg_last_error", "hcg_version",
-           "hcg_operand_in_place", "hcg_tile_load", "hcg_tile_store")
+           "hcg_operand_in_place", "hcg_tile_load", "hcg_tile_store", "hcg_mfma_step")
 
 NOALLOC_SCRATCH_BYTES = 32 << 20  # HCG_NOALLOC_SCRATCH_BYTES
 
@@ -84,6 +84,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.hcg_tile_load.restype = c_int
     lib.hcg_tile_store.argtypes = [c_int, vp, i64, i64, i64, vp, i64, i64, i64, vp, vp, vp]
     lib.hcg_tile_store.restype = c_int
+    lib.hcg_mfma_step.argtypes = [c_int, c_int, c_int, c_int, vp, vp, vp, vp, vp, vp, vp]
+    lib.hcg_mfma_step.restype = c_int
 
 
 def load() -> ctypes.CDLL:
@@ -166,3 +168,11 @@ def tile_store(elem_bytes: int, dst: int, ld: int, rows: int, cols: int, origins
     rc = lib.hcg_tile_store(elem_bytes, dst or None, ld, rows, cols, origins or None, ntiles, th, tw,
                             tiles or None, tile_mask or None, stream or None)
     check(lib, rc, "hcg_tile_store")
+
+
+def mfma_step(dtype: int, m: int, n: int, k: int, a: int, b: int, a_mask: int, b_mask: int, acc_in: int,
+              acc_out: int, stream: int) -> None:
+    lib = load()
+    rc = lib.hcg_mfma_step(dtype, m, n, k, a or None, b or None, a_mask or None, b_mask or None, acc_in or None,
+                           acc_out or None, stream or None)
+    check(lib, rc, "hcg_mfma_step")

@@ -364,9 +364,10 @@ def wmma_clamped(group, a_tile, b_tile, a_frag, b_frag, acc_frag, *, lane, wave_
 
 
 @kernel.intrinsic(scope=WorkItem, effects="pure", const_attrs={"wave_size", "arch"},
-                  result_types=(vector_type((ROWS_PER_LANE,), np.float16),))
+                  result_types=(vector_type((ROWS_PER_LANE,), np.float32),))
 def wmma_f16_result(group, a_tile, b_tile, a_frag, b_frag, acc_frag, *, lane, wave_size, arch):
-    """Sums in float32, returns the accumulator rounded to float16."""
+    """Sums in float32, returns the accumulator rounded to float16 (while it
+    declares a float32 result, so only the value it returns shows it)."""
     _ = (a_frag, b_frag, arch)
     out = _narrow_fold(a_tile, b_tile, acc_frag, lane, wave_size, np.float32, None, np.float16)
     return group.vload(out, shape=(len(out),))
@@ -455,3 +456,55 @@ def f16_result_kernel(
         b_tile = group.load(b[k0 : k0 + TILE, col0 : col0 + TILE], shape=(TILE, TILE))
         acc = f16_result_step(group, a_tile, b_tile, acc)
     store_acc(group, c, row0, col0, acc)
+
+
+# A wave64 kernel whose intrinsic states the 32x32x16 arithmetic but whose
+# amdgpu-gfx950 lowering declares another instruction (32x32x8): the launch
+# must refuse it, since the op it would run is not the one the fallback states.
+
+from hc.gfx950 import kernels as _gfx  # noqa: E402
+from hc.gfx950.kernels import init_acc, store_tile  # noqa: E402
+
+
+@kernel.intrinsic(scope=WorkItem, effects="pure", const_attrs={"wave_size", "arch"},
+                  result_types=(vector_type((_gfx.ACC_REGS,), np.float32),))
+def mfma_k8_gfx950(group, a_tile, b_tile, acc_frag, *, lane, wave_size, arch):
+    """The 32x32x16 fallback of mfma_gfx950."""
+    _ = (wave_size, arch)
+    values = _gfx._lane_fold(a_tile, b_tile, acc_frag, _gfx.lane_acc_rows(lane), _gfx.lane_column(lane), _gfx.MFMA_K)
+    return group.vload(values, shape=(_gfx.ACC_REGS,))
+
+
+@mfma_k8_gfx950.lower(target="amdgpu-gfx950")
+def _lower_k8(ctx, group, a_tile, b_tile, acc_frag, *, lane, wave_size, arch):
+    _ = (group, lane)
+    op = ctx.builder.create("rocdl.mfma.f32.32x32x8", results=[ctx.result_type(0)],
+                            operands=[a_tile, b_tile, acc_frag],
+                            attrs={"arch": arch, "wave_size": wave_size, "m": 32, "n": 32, "k": 8}, loc=ctx.loc)
+    return op.result(0)
+
+
+@kernel.func(scope=WorkGroup)
+def k8_step(group, a_tile, b_tile, acc):
+    @group.workitems
+    def wave(wi):
+        lane = wi.local_id()[0]
+        return mfma_k8_gfx950(group, a_tile, b_tile, acc[:, lane, 0], lane=lane, wave_size=64, arch="gfx950")
+
+    return wave()
+
+
+@kernel(work_shape=(ceil_div(M, 32) * 64, ceil_div(N, 32)), group_shape=(64, 1), subgroup_size=64)
+def wrong_shape_kernel(
+    group,
+    a: Buffer[M, K, np.float16],
+    b: Buffer[K, N, np.float16],
+    c: Buffer[M, N, np.float32],
+) -> None:
+    row0, col0 = group.group_id[0] * 32, group.group_id[1] * 32
+    acc = init_acc(group)
+    for k0 in range(0, a.shape[1], 16):
+        a_tile = group.load(a[row0 : row0 + 32, k0 : k0 + 16], shape=(32, 16))
+        b_tile = group.load(b[k0 : k0 + 16, col0 : col0 + 32], shape=(16, 32))
+        acc = k8_step(group, a_tile, b_tile, acc)
+    store_tile(group, c, row0, col0, acc)

@@ -8,7 +8,8 @@ import numpy as np
 
 from hc import Buffer, WorkGroup, WorkItem, kernel, sym, vector_type
 
-from ._kernels import GEOMETRY, ROWS_PER_LANE, TILE, a_fragment, b_fragment, lane_rows, store_acc, tile_origin, zero_acc
+from ._kernels import (GEOMETRY, ROWS_PER_LANE, TILE, _lower_wmma, a_fragment, b_fragment, lane_rows, store_acc,
+                       tile_origin, zero_acc)
 
 M = sym.M
 N = sym.N
@@ -32,8 +33,10 @@ def wmma_doubled(group, a_tile, b_tile, a_frag, b_frag, acc_frag, *, lane, wave_
 
 
 @wmma_doubled.lower(target="amdgpu-gfx11")
-def _lower(ctx, *args, **kwargs):
-    return None
+def _lower(ctx, group, a_tile, b_tile, a_frag, b_frag, acc_frag, *, lane, wave_size, arch):
+    # A well-formed WMMA lowering: only the fallback's doubled product is wrong.
+    return _lower_wmma(ctx, group, a_tile, b_tile, a_frag, b_frag, acc_frag, lane=lane, wave_size=wave_size,
+                       arch=arch)
 
 
 @kernel.func(scope=WorkGroup)

@@ -13,7 +13,7 @@ import pytest
 from hc.gfx950 import _native
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("hcg_gemm.h", "hcg_tile_ops.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("hcg_gemm.h", "hcg_tile_ops.h", "hcg_mfma.h")]
 
 
 def declared_functions() -> list[str]:
@@ -156,3 +156,19 @@ def test_operand_query_without_device_memory():
     assert q(page + 4096 - 2 * 11 - 2, 1, 11, 11) == 0
     assert q(None, 1, 1, 1) == -1 and "NULL" in _native.last_error(lib)
     assert q(0x10000, 2, 8, 7) == -1 and "ld 7" in _native.last_error(lib)
+
+
+@pytest.mark.parametrize(
+    "args,match",
+    [
+        ((2, 32, 32, 16, 0x1000, 0x1000, None, None, 0x1000, 0x1000, None), "dtype must be"),
+        ((0, 32, 32, 8, 0x1000, 0x1000, None, None, 0x1000, 0x1000, None), "32 x 32 x 8"),
+        ((1, 16, 16, 16, 0x1000, 0x1000, None, None, 0x1000, 0x1000, None), "16 x 16 x 16"),
+        ((0, 16, 16, 32, None, 0x1000, None, None, 0x1000, 0x1000, None), "must not be NULL"),
+        ((0, 32, 32, 16, 0x1000, 0x1000, None, None, 0x1000, None, None), "must not be NULL"),
+    ],
+)
+def test_mfma_step_rejects_bad_arguments_on_the_host(args, match):
+    lib = _native.load()
+    assert lib.hcg_mfma_step(*args) == _native.HCG_EINVAL
+    assert re.search(match, _native.last_error(lib))

@@ -161,6 +161,113 @@ def test_the_package_kernels_are_recognised_through_their_mfma_intrinsic():
                       (kernels.tiled_gfx950_mfma_matmul_bf16, "bfloat16")):
         got = _contract.recognise(fn)
         assert got.tile == (32, 32, 16) and got.dtype == dtype and got.intrinsics == ("mfma_gfx950",)
+        assert got.ops == ("rocdl.mfma.f32.32x32x16",)
+    for fn, dtype in ((kernels.tiled_gfx950_mfma16_matmul, "float16"),
+                      (kernels.tiled_gfx950_mfma16_matmul_bf16, "bfloat16")):
+        got = _contract.recognise(fn)
+        assert got.tile == (16, 16, 32) and got.dtype == dtype and got.intrinsics == ("mfma16_gfx950",)
+        assert got.ops == ("rocdl.mfma.f32.16x16x32",)
+    assert _contract.recognise(_kernels.tiled_gfx11_wmma_matmul).ops == ("amdgpu.wmma",)
+
+
+def _wave_inputs(m, n, k, seed, dtype="float16", ints=False):
+    rng = np.random.default_rng(seed)
+    if ints:
+        a = rng.integers(-8, 9, (m, k)).astype(np.float32)
+        b = rng.integers(-8, 9, (k, n)).astype(np.float32)
+    else:
+        a = rng.normal(0, 1, (m, k)).astype(np.float32)
+        b = rng.normal(0, 1, (k, n)).astype(np.float32)
+    if dtype == "float16":
+        a, b = a.astype(np.float16), b.astype(np.float16)
+    else:
+        from hc.gfx950.workloads import f32_to_bf16_bits
+
+        a, b = f32_to_bf16_bits(a), f32_to_bf16_bits(b)
+    return a, b, rng.random((m, k)) < 0.8, rng.random((k, n)) < 0.8
+
+
+def test_fallback_wave_of_both_intrinsics_is_one_masked_matrix_step():
+    """fallback_wave runs the fallback body per lane; placed by the stated
+    lane layout the 64 results are acc + A @ B of the masked operands, as the
+    oracle's sequential float32 fold (every intrinsic, both dtypes)."""
+    import hc_oracle as oracle
+    from hc.gfx950 import intrinsics, kernels
+
+    cases = ((kernels.mfma_gfx950, 32, 16, kernels.lane_acc_rows, kernels.lane_column),
+             (kernels.mfma16_gfx950, 16, 32, kernels.lane16_acc_rows, kernels.lane16_column))
+    for fn, mn, k, rows_of, col_of in cases:
+        for dtype in ("float16", "bfloat16"):
+            a, b, am, bm = _wave_inputs(mn, mn, k, 5, dtype)
+            code = oracle.F16 if dtype == "float16" else oracle.BF16
+            a0 = np.where(am, a, np.zeros_like(a))
+            b0 = np.where(bm, b, np.zeros_like(b))
+            regs = mn * mn // 64
+            got = intrinsics.fallback_wave(fn, a, b, np.zeros((64, regs), np.float32), dtype=dtype, a_mask=am,
+                                           b_mask=bm, wave_size=64, arch="gfx950")
+            c = np.full((mn, mn), np.nan, np.float32)
+            for lane in range(64):
+                for r, row in enumerate(rows_of(lane)):
+                    c[row, col_of(lane)] = got[lane, r]
+            assert np.array_equal(c, oracle.gemm_sequential(a0, b0, code)), (fn.__name__, dtype)
+
+
+def test_lowering_is_called_through_a_recording_ctx():
+    from hc.gfx950 import intrinsics, kernels
+
+    for fn, shape in ((kernels.mfma_gfx950, (32, 32, 16)), (kernels.mfma16_gfx950, (16, 16, 32))):
+        m, n, k = shape
+        a, b, _, _ = _wave_inputs(m, n, k, 1)
+        name, got = intrinsics.lowered_op(fn, a, b, np.zeros((64, m * n // 64), np.float32), wave_size=64,
+                                          arch="gfx950")
+        assert got == shape and name == f"rocdl.mfma.f32.{m}x{n}x{k}"
+    # another instruction, declared by an intrinsic's lowering: refused before any device call
+    a, b, _, _ = _wave_inputs(32, 32, 16, 1)
+    with pytest.raises(LaunchError, match=r"creates 'rocdl.mfma.f32.32x32x8', which no kernel of this library"):
+        intrinsics.run_wave(_kernels.mfma_k8_gfx950, a, b, np.zeros((64, 16), np.float32), wave_size=64,
+                            arch="gfx950")
+
+
+def test_lowerings_that_misstate_the_op_are_refused():
+    from hc.core import vector_type
+    from hc.gfx950 import _lowering, kernels
+
+    args = ("group", "a", "b", "acc")
+
+    def intrinsic_with(lower):
+        @kernel.intrinsic(scope=WorkItem, effects="pure", const_attrs={"wave_size", "arch"},
+                          result_types=(vector_type((16,), np.float32),))
+        def probe_mfma(group, a_tile, b_tile, acc_frag, *, lane, wave_size, arch):
+            return acc_frag
+
+        probe_mfma.lower(target="amdgpu-gfx950")(lower)
+        return probe_mfma
+
+    def op(ctx, name="rocdl.mfma.f32.32x32x16", results=None, operands=None, **attrs):
+        full = {"arch": "gfx950", "wave_size": 64, "m": 32, "n": 32, "k": 16, **attrs}
+        return ctx.builder.create(name, results=results if results is not None else [ctx.result_type(0)],
+                                  operands=operands if operands is not None else ["a", "b", "acc"], attrs=full,
+                                  loc=ctx.loc)
+
+    def check(lower, match):
+        fn = intrinsic_with(lower)
+        with pytest.raises(_lowering.LoweringError, match=match):
+            recorded = _lowering.record_lowering(fn, "amdgpu-gfx950", args, {"lane": 0, "wave_size": 64,
+                                                                            "arch": "gfx950"})
+            _lowering.check_matrix_op(recorded, "amdgpu-gfx950", fn, args)
+
+    check(lambda ctx, *a, **k: op(ctx, k=8).result(0), r"declares k=8, but that instruction has k=16")
+    check(lambda ctx, *a, **k: op(ctx, arch="gfx942").result(0), r"declares arch='gfx942'")
+    check(lambda ctx, *a, **k: op(ctx, wave_size=32).result(0), r"declares wave_size=32")
+    check(lambda ctx, *a, **k: op(ctx, name="rocdl.mfma.f32.16x16x32", m=16, n=16, k=32).result(0),
+          r"results are .*not one VectorTypeSpec\(dimensions=\(4,\)")
+    check(lambda ctx, *a, **k: op(ctx, operands=["acc", "b", "a"]).result(0), "accumulator")
+    check(lambda ctx, *a, **k: (op(ctx), op(ctx))[0].result(0), "creates 2 ops")
+    check(lambda ctx, *a, **k: op(ctx) and None, "does not return result 0")
+    check(lambda ctx, *a, **k: ctx.builder.create("rocdl.mfma.f32.32x32x16", results=[ctx.result_type(1)]),
+          "declares 1 result types")
+    assert _lowering.lowering_target(kernels.mfma_gfx950) == "amdgpu-gfx950"
+    assert _lowering.lowering_target(_kernels.wmma_gfx11) == "amdgpu-gfx11"
 
 
 @pytest.mark.parametrize(
@@ -176,6 +283,7 @@ def test_the_package_kernels_are_recognised_through_their_mfma_intrinsic():
         ("f16_fold_kernel", r"probe with partial sums that need float32 accumulation computes \d+ elements"),
         ("clamped_kernel", r"probe with partial sums that need float32 accumulation computes \d+ elements"),
         ("f16_result_kernel", "helper 'f16_result_step' returns a float16 accumulator, not float32"),
+        ("wrong_shape_kernel", r"creates 'rocdl.mfma.f32.32x32x8', which no kernel of this library executes"),
     ],
 )
 def test_near_misses_are_rejected_with_the_reason(name, reason):
