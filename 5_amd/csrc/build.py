@@ -6,8 +6,9 @@ compiles 5_amd/csrc/hcg_gemm.hip, hcg_tile.hip and hcg_mfma.hip (kernels +
 the C ABI declared in include/hcg_gemm.h, include/hcg_tile_ops.h and
 include/hcg_mfma.h) with hipcc for
 gfx950 into
-5_amd/hc/gfx950/libhcg_gfx950.so, next to the Python code that loads it,
-and hcg_probe.hip (the hardware ceiling probes of include/hcg_probe.h, used
+5_amd/hc/gfx950/libhcg_gfx950.so, next to the Python code that loads it
+(and, with -DHCG_STAMPS, libhcg_gfx950_stamps.so, whose GEMM kernels record
+per-workgroup timestamps for bench.py --stamps), and hcg_probe.hip (the hardware ceiling probes of include/hcg_probe.h, used
 by bench.py) into 5_amd/hc/gfx950/libhcg_probe.so, and hcg_torch.cpp (host
 code: the device-tensor binding of hcg_gemm_algo as a Python extension,
 linked against libhcg_gfx950.so) with g++ against the installed PyTorch into
@@ -29,6 +30,9 @@ ROOT = os.path.dirname(PKG)
 SRCS = [os.path.join(HERE, f) for f in ("hcg_gemm.hip", "hcg_tile.hip", "hcg_mfma.hip")]
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(PKG, "hc", "gfx950", "libhcg_gfx950.so")
+# The same sources with -DHCG_STAMPS: the tiled and streaming kernels record
+# per-workgroup timestamps (bench.py --stamps); never loaded by the package.
+STAMPS_OUT = os.path.join(PKG, "hc", "gfx950", "libhcg_gfx950_stamps.so")
 PROBE_SRCS = [os.path.join(HERE, "hcg_probe.hip")]
 PROBE_OUT = os.path.join(PKG, "hc", "gfx950", "libhcg_probe.so")
 TORCH_SRC = os.path.join(HERE, "hcg_torch.cpp")
@@ -60,22 +64,28 @@ def flags() -> list[str]:
     ]
 
 
-def _compile(srcs: list[str], out: str, verbose: bool) -> str:
+def _start(srcs: list[str], out: str, extra: list[str], verbose: bool) -> tuple[subprocess.Popen, str]:
     os.makedirs(os.path.dirname(out), exist_ok=True)
     tmp = out + ".tmp"
-    cmd = [hipcc(), *flags(), *srcs, "-o", tmp]
+    cmd = [hipcc(), *flags(), *extra, *srcs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
+    proc = subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+    return proc, out
+
+
+def _finish(job: tuple[subprocess.Popen, str], verbose: bool) -> str:
+    proc, out = job
+    _, stderr = proc.communicate()
     # The host pass does not know the device-only target feature; that
     # warning is expected and harmless.  Anything else is shown.
     noise = "'-packed-fp32-ops' is not a recognized feature for this target"
-    err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    err = "\n".join(line for line in stderr.splitlines() if noise not in line)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
+        raise RuntimeError(f"hipcc failed for {os.path.basename(out)} ({proc.returncode}):\n{err}")
     if verbose and err.strip():
         print(err)
-    os.replace(tmp, out)
+    os.replace(out + ".tmp", out)
     return out
 
 
@@ -107,12 +117,14 @@ def _compile_torch_binding(verbose: bool) -> str:
 
 
 def build(verbose: bool = False) -> str:
-    """Builds the GEMM library, the probe library and the device-tensor
-    binding; returns the first."""
-    out = _compile(SRCS, OUT, verbose)
-    _compile(PROBE_SRCS, PROBE_OUT, verbose)
+    """Builds the GEMM library, its timestamped variant, the probe library
+    and the device-tensor binding (the three hipcc runs in parallel);
+    returns the first."""
+    jobs = [_start(SRCS, OUT, [], verbose), _start(SRCS, STAMPS_OUT, ["-DHCG_STAMPS"], verbose),
+            _start(PROBE_SRCS, PROBE_OUT, [], verbose)]
+    outs = [_finish(job, verbose) for job in jobs]
     _compile_torch_binding(verbose)
-    return out
+    return outs[0]
 
 
 if __name__ == "__main__":

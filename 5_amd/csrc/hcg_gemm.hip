@@ -361,6 +361,51 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
+// Per-workgroup timing records, in the HCG_STAMPS build of this file only
+// (libhcg_gfx950_stamps.so; in the product build every member is empty).
+// mark(i) reads the 100 MHz constant clock (s_memrealtime) and the shader
+// clock (s_memtime) at the workgroup's start (0), the end of its prologue
+// (1), the end of its K loop (2); write() waits for the workgroup's stores
+// to be acknowledged, marks its end (3) and has lane 0 store, with vector
+// stores, one record of 8 words at g_stamp_buf + 8 * blockIdx.x:
+//   [0..3] clock at marks 0..3, [4] shader cycles of the K loop (2 - 1),
+//   [5] shader cycles start to end (3 - 0), [6] XCC id, [7] HW_ID.
+// hcg_stamps_set() names the buffer; bench.py --stamps reads it.
+#ifdef HCG_STAMPS
+__device__ uint64_t* g_stamp_buf = nullptr;
+__device__ int64_t g_stamp_cap = 0;
+#endif
+struct WgStamps {
+#ifdef HCG_STAMPS
+  uint64_t t[4] = {}, c[4] = {};
+  __device__ __forceinline__ void mark(int i) {
+    t[i] = __builtin_amdgcn_s_memrealtime();
+    c[i] = __builtin_amdgcn_s_memtime();
+  }
+  __device__ __forceinline__ void write() {
+    wait_vmcnt<0>();
+    mark(3);
+    uint64_t* buf = g_stamp_buf;
+    if (threadIdx.x == 0 && buf != nullptr && (int64_t)blockIdx.x < g_stamp_cap) {
+      const uint64_t xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20);  // HW_REG_XCC_ID[3:0]
+      const uint64_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);   // HW_REG_HW_ID
+      uint64_t* r = buf + 8 * (int64_t)blockIdx.x;
+      r[0] = t[0];
+      r[1] = t[1];
+      r[2] = t[2];
+      r[3] = t[3];
+      r[4] = c[2] - c[1];
+      r[5] = c[3] - c[0];
+      r[6] = xcc;
+      r[7] = hw;
+    }
+  }
+#else
+  __device__ __forceinline__ void mark(int) {}
+  __device__ __forceinline__ void write() {}
+#endif
+};
+
 template <int TM>
 constexpr int dma_stage_bytes() {
   return (TM + kTileN) * kDmaK * 2;
@@ -472,6 +517,8 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
   constexpr int kDmaPerWave = kADma + 4;  // + 4 for B
   constexpr int kABytes = TM * kDmaK * 2;
 
+  WgStamps stamps;
+  stamps.mark(0);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   // Wave index as a provably uniform value: it feeds the LDS base (M0) of
@@ -794,6 +841,7 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
   }
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
+  stamps.mark(1);
   read_frags(StageC<0>{}, 0, fa0, fb0);
   if constexpr (KT) mask_tail(fa0, 0, 0);
 
@@ -821,6 +869,7 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
     if (kt < nk) iteration(StageC<2>{}, Checked{}, kt++);
   // No DMA may still be writing LDS when the workgroup retires.
   wait_vmcnt<0>();
+  stamps.mark(2);
 
   // Epilogue.  The accumulators go through LDS so that C leaves in full
   // 512-byte row segments (32 lanes x 16 bytes) instead of 4-byte scatters.
@@ -895,6 +944,7 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
+  stamps.write();
 }
 
 // Copies of up to two rows x cols 16-bit matrices (row stride ld) into
@@ -1357,6 +1407,8 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
     nb = 8 * q + ((x + q + split) & 7);
   }
   if (nb * NB >= g.N) return;
+  WgStamps stamps;
+  stamps.mark(0);
   const int n0 = nb * NB;
   const int kbeg = split * g.kchunk;
   const int kend = min(g.K, kbeg + g.kchunk);
@@ -1551,6 +1603,7 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
   if constexpr (PF > 5) issue(StageC<5>{}, 5);
   if constexpr (PF > 6) issue(StageC<6>{}, 6);
 
+  stamps.mark(1);
   int step = 0;
   for (; step + kStStages <= nsteps; step += kStStages) {
     step_fn(StageC<0>{}, step);
@@ -1570,6 +1623,7 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
   if (step < nsteps) step_fn(StageC<5>{}, step++);
   if (step < nsteps) step_fn(StageC<6>{}, step++);
   wait_vmcnt<0>();  // no DMA may still be writing LDS at exit
+  stamps.mark(2);
 
   // 16x16 accumulator layout: register r of lane l holds row 4*(l/16) + r,
   // column l%16 of the block.
@@ -1584,11 +1638,13 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
           const int row = 16 * rb + (lane >> 4) * 4 + r, col = ocol + 16 * j;
           if (row < g.M && col < g.N) g.C[(int64_t)row * g.ldc + col] = acc[rb][j][r];
         }
+    stamps.write();
     return;
   }
   if constexpr (R <= 2) {
     if (g.counters != nullptr) {
       stream_fused_reduce<R>(g, acc, nb, split);
+      stamps.write();
       return;
     }
   }
@@ -1601,6 +1657,7 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
         const int row = 16 * rb + (lane >> 4) * 4 + r, col = ocol + 16 * j;
         if (col < g.N) g.ws[((int64_t)split * 16 * R + row) * g.N + col] = acc[rb][j][r];
       }
+  stamps.write();
 }
 
 // ---------------------------------------------------------------------------
@@ -3107,6 +3164,20 @@ int hcg_gemm_noalloc(int dtype, const void* A, int64_t lda, const void* B, int64
 const char* hcg_last_error(void) { return t_last_error.c_str(); }
 
 int hcg_version(void) { return 100; }
+
+#ifdef HCG_STAMPS
+// The HCG_STAMPS build only (no counterpart in the reference; for bench.py
+// --stamps): the device buffer of `records` 8-word records that the tiled and
+// streaming GEMM kernels fill, record b for workgroup b (NULL: none).
+int hcg_stamps_set(void* buf, int64_t records) {
+  t_last_error.clear();
+  uint64_t* p = static_cast<uint64_t*>(buf);
+  const int64_t cap = buf ? records : 0;
+  HCG_HIP_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(g_stamp_buf), &p, sizeof p));
+  HCG_HIP_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(g_stamp_cap), &cap, sizeof cap));
+  return HCG_OK;
+}
+#endif
 
 int hcg_operand_in_place(const void* base, int64_t rows, int64_t cols, int64_t ld) {
   t_last_error.clear();

@@ -19,7 +19,10 @@ metric configuration, fp16 M=N=K=4096; ``value`` is TFLOP/s
   bytes against the 8 TB/s HBM peak, timed while rotating through enough
   copies of B that every launch streams B from HBM, not from the 256 MB
   Infinity Cache (warm, same-buffer numbers are reported beside it);
-* ``others``: the remaining BASELINE.json configurations, TFLOP/s;
+* ``others``: the remaining BASELINE.json configurations, TFLOP/s, each
+  also ``cold``: A and B rotated over copies larger than the Infinity Cache
+  (``cold`` at the top level is the headline workload's; ``value`` is the
+  warm figure, the same operands every launch);
 * ``board``: graphics (per XCD too) and memory clocks and socket power
   sampled from the driver while the headline workload runs;
 * ``ceiling``: what this board sustains, measured in the same run by the
@@ -28,7 +31,9 @@ metric configuration, fp16 M=N=K=4096; ``value`` is TFLOP/s
   ``skinny`` carry ``frac_of_ceiling`` beside ``frac`` (which stays against
   the 2516.6 TFLOP/s and 8 TB/s nameplate peaks).
 
-``--ceilings-only`` runs just the probes (for rocprofv3).
+``--ceilings-only`` runs just the probes (for rocprofv3).  ``--stamps
+WORKLOAD`` runs a workload through the timestamped build of the library and
+prints where one sustained launch's time goes (hc/gfx950/stamps.py).
 """
 
 from __future__ import annotations
@@ -76,6 +81,12 @@ def parse_args() -> argparse.Namespace:
                         "runs (as under a tracer), and print their event time per launch")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="run 5 device-to-device copies of MIB MiB (calibrates FETCH_SIZE/WRITE_SIZE) and exit")
+    p.add_argument("--stamps", metavar="WORKLOAD",
+                   help="run WORKLOAD through the timestamped build of the library (libhcg_gfx950_stamps.so) "
+                        "and print where its last sustained launch's time goes, per workgroup and per XCD")
+    p.add_argument("--stamps-copies", type=int, default=0, metavar="N",
+                   help="with --stamps: rotate A and B over N copies (default: 5 for c4_skinny_f16, whose B the "
+                        "bench streams from HBM, else 1)")
     return p.parse_args()
 
 
@@ -399,6 +410,35 @@ def first_use(torch, g, stream) -> dict:
     return out
 
 
+def bench_cold(torch, g, stream, name: str, steps: int, warmup: int) -> dict:
+    """Event time per launch with A and B rotated over copies that total at
+    least twice the 256 MB Infinity Cache, so every launch reads its operands
+    from HBM (the warm figures reuse one pair of operands, which then stays
+    in the Infinity Cache when it fits)."""
+    from hc.gfx950.workloads import CONFIGS, make_inputs, to_torch
+
+    cfg = CONFIGS[name]
+    dev = torch.device("cuda", 0)
+    a, b = make_inputs(cfg, seed=0)
+    ta0, tb0 = to_torch(a, cfg.dtype, dev), to_torch(b, cfg.dtype, dev)
+    pair = 2 * (ta0.numel() + tb0.numel())
+    copies = max(2, math.ceil(2 * MALL_BYTES / pair))
+    tas = [ta0] + [ta0.clone() for _ in range(copies - 1)]
+    tbs = [tb0] + [tb0.clone() for _ in range(copies - 1)]
+    tc = torch.empty((cfg.m, cfg.n), dtype=torch.float32, device=dev)
+    it = {"i": 0}
+
+    def rotating():
+        i = it["i"] % copies
+        it["i"] += 1
+        g.gemm(tas[i], tbs[i], out=tc)
+
+    t, _ = time_launches(torch, stream, rotating, steps, warmup)
+    del tas, tbs
+    return {"value": cfg.flops / t / 1e12, "unit": "TFLOP/s", "us_per_launch": t * 1e6, "operand_copies": copies,
+            "operand_bytes_rotated": copies * pair}
+
+
 def bench_config(torch, g, stream, name: str, steps: int, warmup: int) -> dict:
     from hc.gfx950.workloads import CONFIGS, make_inputs, to_torch
 
@@ -441,6 +481,15 @@ def main() -> int:
     cfg = CONFIGS[args.workload]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.stamps:
+        from hc.gfx950 import stamps
+
+        name = args.stamps
+        copies = args.stamps_copies or (5 if name == "c4_skinny_f16" else 1)
+        log(f"stamps: {name}, operands rotated over {copies} cop{'y' if copies == 1 else 'ies'}")
+        out = stamps.run(torch, name, copies=copies, warm_s=max(0.3, WARM_S), algo=2 if name == "c4_skinny_f16" else 0)
+        print(json.dumps({"stamps": out}), flush=True)
+        return 0
     stream = torch.cuda.Stream(device=dev)
     if args.copy_probe:
         n = args.copy_probe * 1024 * 1024 // 4
@@ -514,6 +563,8 @@ def main() -> int:
     roofline["traffic"], roofline["traffic_source"] = measured_traffic(kernel_name, cfg.name)
     roofline["per_launch_us"] = per_launch * 1e6
     roofline["median_single_launch_us"] = median_launch(torch, stream, step, 200) * 1e6
+    roofline["timing"] = ("warm: the same A and B every launch" if not is_skinny else
+                          "cold: B rotated over copies larger than the Infinity Cache")
     roofline["algorithmic_per_launch"] = cfg.algorithmic_bytes if is_skinny else cfg.flops
 
     result = {
@@ -546,6 +597,11 @@ def main() -> int:
         "board": board_state(torch, stream, step, 2.5),
     }
     del ta, tb, tc
+    if not args.no_extra and not is_skinny:
+        log(f"bench: {cfg.name} cold (operands rotated)")
+        cold = bench_cold(torch, g, stream, cfg.name, args.steps, args.warmup)
+        cold["note"] = "value uses the warm figure; this one reads A and B from HBM on every launch"
+        result["cold"] = cold
     if not args.no_extra:
         log("bench: skinny M=16 (rotating B buffers)")
         result["skinny"] = bench_skinny(torch, g, stream, max(20, args.steps), max(5, args.warmup // 2))
@@ -555,6 +611,8 @@ def main() -> int:
                 continue
             log(f"bench: {name}")
             others[name] = bench_config(torch, g, stream, name, max(20, args.steps // 4), 5)
+            if name != "c1_128_f16":
+                others[name]["cold"] = bench_cold(torch, g, stream, name, max(20, args.steps // 4), 5)
         result["others"] = others
     if fresh is not None:
         result["first_use"] = fresh

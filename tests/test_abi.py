@@ -172,3 +172,29 @@ def test_mfma_step_rejects_bad_arguments_on_the_host(args, match):
     lib = _native.load()
     assert lib.hcg_mfma_step(*args) == _native.HCG_EINVAL
     assert re.search(match, _native.last_error(lib))
+
+
+def test_stamps_library_is_built_apart_and_its_records_reduce():
+    """The timestamped build exports hcg_stamps_set (the product library does
+    not), and breakdown() reduces records: two CUs of one XCD, one running two
+    workgroups in sequence, at a 2.0 GHz shader clock."""
+    import numpy as np
+
+    from hc.gfx950 import stamps
+
+    assert os.path.exists(stamps.LIB_PATH), "run 5_amd/csrc/build.py"
+    assert not hasattr(_native.load(), "hcg_stamps_set")
+    assert hasattr(ctypes.CDLL(stamps.LIB_PATH), "hcg_stamps_set")
+
+    def rec(t0, t1, t2, t3, cu):
+        return [t0, t1, t2, t3, 2 * (t2 - t1) * 10, 2 * (t3 - t0) * 10, 3, cu << 8]
+
+    r = np.array([rec(1000, 1100, 2100, 2300, 1), rec(1010, 1110, 2010, 2210, 2), rec(2400, 2500, 3500, 3700, 1),
+                  [0] * 8], dtype=np.uint64)
+    out = stamps.breakdown(r)
+    assert out["workgroups"] == 3
+    assert out["span_us"] == 27.0
+    assert out["k_loop_us"] == {"mean": 29.0 / 3, "min": 9.0, "max": 10.0}
+    assert out["per_xcd"][0]["xcd"] == 3 and abs(out["per_xcd"][0]["clock_mhz"] - 2000) < 1e-9
+    assert out["cu_rounds"] == {"cus": 2, "max_per_cu": 2, "min_per_cu": 1, "mean_gap_us": 1.0}
+    assert out["start_spread_us"] == 0.1
