@@ -313,6 +313,9 @@ struct FastArgs {
   int splits, kchunk;
   float* ws;
   bool ws_vec;           // N is a multiple of 4 (16-byte partial rows)
+#ifdef HCG_STAMPS
+  int stamp_slot;
+#endif
 };
 
 // Scheduling-group masks for __builtin_amdgcn_sched_group_barrier.
@@ -369,15 +372,30 @@ __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f
 // to be acknowledged, marks its end (3) and has lane 0 store, with vector
 // stores, one record of 8 words at g_stamp_buf + 8 * blockIdx.x:
 //   [0..3] clock at marks 0..3, [4] shader cycles of the K loop (2 - 1),
-//   [5] shader cycles start to end (3 - 0), [6] XCC id, [7] HW_ID.
-// hcg_stamps_set() names the buffer; bench.py --stamps reads it.
+//   [5] shader cycles start to end (3 - 0), [6] XCC id (bits 3:0), grid size
+//   (bits 47:8) and record slot (bit 48), [7] HW_ID.
+// hcg_stamps_set() names the buffer; bench.py --stamps reads it.  Launches
+// alternate between two record areas (slot 0 at record blockIdx.x, slot 1 at
+// gridDim.x + blockIdx.x), so two consecutive launches can be compared.
 #ifdef HCG_STAMPS
 __device__ uint64_t* g_stamp_buf = nullptr;
 __device__ int64_t g_stamp_cap = 0;
+int g_stamp_launches = 0;  // host: launches so far (their parity is the slot)
+#define HCG_STAMP_SLOT(g) (g).stamp_slot
+#define HCG_STAMP_ARGS(Args, a) \
+  Args a##_s = a;               \
+  a##_s.stamp_slot = g_stamp_launches++ & 1;
+#define HCG_STAMPED(a) a##_s
+#else
+#define HCG_STAMP_SLOT(g) 0
+#define HCG_STAMP_ARGS(Args, a)
+#define HCG_STAMPED(a) a
 #endif
 struct WgStamps {
 #ifdef HCG_STAMPS
+  int slot;
   uint64_t t[4] = {}, c[4] = {};
+  __device__ explicit WgStamps(int s) : slot(s) {}
   __device__ __forceinline__ void mark(int i) {
     t[i] = __builtin_amdgcn_s_memrealtime();
     c[i] = __builtin_amdgcn_s_memtime();
@@ -386,21 +404,23 @@ struct WgStamps {
     wait_vmcnt<0>();
     mark(3);
     uint64_t* buf = g_stamp_buf;
-    if (threadIdx.x == 0 && buf != nullptr && (int64_t)blockIdx.x < g_stamp_cap) {
+    const int64_t index = (int64_t)blockIdx.x + (int64_t)gridDim.x * slot;
+    if (threadIdx.x == 0 && buf != nullptr && index < g_stamp_cap) {
       const uint64_t xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20);  // HW_REG_XCC_ID[3:0]
       const uint64_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);   // HW_REG_HW_ID
-      uint64_t* r = buf + 8 * (int64_t)blockIdx.x;
+      uint64_t* r = buf + 8 * index;
       r[0] = t[0];
       r[1] = t[1];
       r[2] = t[2];
       r[3] = t[3];
       r[4] = c[2] - c[1];
       r[5] = c[3] - c[0];
-      r[6] = xcc;
+      r[6] = xcc | ((uint64_t)gridDim.x << 8) | ((uint64_t)slot << 48);
       r[7] = hw;
     }
   }
 #else
+  __device__ explicit WgStamps(int) {}
   __device__ __forceinline__ void mark(int) {}
   __device__ __forceinline__ void write() {}
 #endif
@@ -517,7 +537,7 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
   constexpr int kDmaPerWave = kADma + 4;  // + 4 for B
   constexpr int kABytes = TM * kDmaK * 2;
 
-  WgStamps stamps;
+  WgStamps stamps(HCG_STAMP_SLOT(g));
   stamps.mark(0);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -915,13 +935,33 @@ __global__ __launch_bounds__(kTiledThreads, TM == 256 ? 1 : 2) void gemm_dma_ker
           float* dst = g.C + (int64_t)grow * g.ldc + gcol;
           if (col_live) __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst));
         }
+      } else if (g.c_vec && (g.N & 3) == 0) {
+        // Edge tiles of 16-byte aligned C rows with N a multiple of 4 (every
+        // chunk whole): non-temporal as in full tiles, rows past M and chunks
+        // past N skipped.  Plain stores leave dirty L2 lines that the end of
+        // the launch must write back: 4096 x 3008 x 1024 took 34.1-34.4 us per
+        // launch with its last tile column stored plainly, 31.7 us this way
+        // (per-workgroup stamps: 7.6 -> 4.1 us from the last workgroup's end
+        // to the next launch's start).  A chunk straddling N would mix plain
+        // element stores into a line written non-temporally, which cost more
+        // (2000 x 3003 x 1000, ldc 3004: 24.1 -> 25.5 us), so those tiles
+        // keep the path below.
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int lr = 2 * i + (lane >> 5);
+          const f32x4 v = *reinterpret_cast<const f32x4*>(ep + lr * kEpRow + c4);
+          const int grow = m0 + wm * (TM / 2) + mi * 32 + hh * 16 + lr;
+          float* dst = g.C + (int64_t)grow * g.ldc + gcol;
+          if (col_live && grow < g.M && gcol < g.N) __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst));
+        }
       } else {
-        // Edge tiles and C rows without 16-byte alignment: the same lane
-        // layout, 16-byte stores at 4-byte aligned addresses (C is float, so
-        // every address is; gfx950 takes unaligned vector stores), rows past
-        // M skipped and a chunk reaching past N stored element by element.
-        // (4-byte stores of one column per lane ran 1.4 us slower on
-        // 4095 x 3001 x 1027, whose C rows are 12004 bytes apart.)
+        // C rows without 16-byte alignment: the same lane layout, 16-byte
+        // stores at 4-byte aligned addresses (C is float, so every address
+        // is; gfx950 takes unaligned vector stores), rows past M skipped and
+        // a chunk reaching past N stored element by element.  (4-byte stores
+        // of one column per lane ran 1.4 us slower on 4095 x 3001 x 1027,
+        // whose C rows are 12004 bytes apart; non-temporal stores at these
+        // addresses, or write-through ones, made its epilogue 5-13 us longer.)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int lr = 2 * i + (lane >> 5);
@@ -1205,6 +1245,9 @@ struct StreamArgs {
   bool c_vec;     // C rows 16-byte aligned at every 4th column
   unsigned* counters;  // per column block arrival counters (all zero between launches), or null
   int ws_bytes;        // bytes of the partials (with counters: below 2^31)
+#ifdef HCG_STAMPS
+  int stamp_slot;
+#endif
 };
 
 #define HCG_ST_STAGE(i) \
@@ -1407,7 +1450,7 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(StreamArgs g) {
     nb = 8 * q + ((x + q + split) & 7);
   }
   if (nb * NB >= g.N) return;
-  WgStamps stamps;
+  WgStamps stamps(HCG_STAMP_SLOT(g));
   stamps.mark(0);
   const int n0 = nb * NB;
   const int kbeg = split * g.kchunk;
@@ -2470,15 +2513,16 @@ template <int DT, bool WIDE, bool KT = false>
 int launch_dma(const FastArgs& a, int shape, hipStream_t stream) {
   const dim3 grid((unsigned)(a.tiles_m * a.tiles_n * (a.splits > 1 ? a.splits : 1)));
   const dim3 block(kTiledThreads);
+  HCG_STAMP_ARGS(FastArgs, a)
   // 256-row tiles move A as 64-wide K pairs (A2) unless the operands need
   // the WIDE form.
   constexpr bool kA2 = !WIDE;
   switch (shape) {
-    case 0: gemm_dma_kernel<DT, 256, 256, 4, WIDE, KT, kA2><<<grid, block, 0, stream>>>(a); break;
-    case 1: gemm_dma_kernel<DT, 256, 192, 4, WIDE, KT, kA2><<<grid, block, 0, stream>>>(a); break;
-    case 2: gemm_dma_kernel<DT, 128, 256, 3, WIDE, KT><<<grid, block, 0, stream>>>(a); break;
-    case 3: gemm_dma_kernel<DT, 128, 128, 3, WIDE, KT><<<grid, block, 0, stream>>>(a); break;
-    default: gemm_dma_kernel<DT, 256, 64, 4, WIDE, KT, kA2><<<grid, block, 0, stream>>>(a); break;
+    case 0: gemm_dma_kernel<DT, 256, 256, 4, WIDE, KT, kA2><<<grid, block, 0, stream>>>(HCG_STAMPED(a)); break;
+    case 1: gemm_dma_kernel<DT, 256, 192, 4, WIDE, KT, kA2><<<grid, block, 0, stream>>>(HCG_STAMPED(a)); break;
+    case 2: gemm_dma_kernel<DT, 128, 256, 3, WIDE, KT><<<grid, block, 0, stream>>>(HCG_STAMPED(a)); break;
+    case 3: gemm_dma_kernel<DT, 128, 128, 3, WIDE, KT><<<grid, block, 0, stream>>>(HCG_STAMPED(a)); break;
+    default: gemm_dma_kernel<DT, 256, 64, 4, WIDE, KT, kA2><<<grid, block, 0, stream>>>(HCG_STAMPED(a)); break;
   }
   HCG_HIP_CHECK(hipGetLastError());
   return HCG_OK;
@@ -2553,16 +2597,17 @@ int launch_stream(const StreamArgs& a, hipStream_t stream) {
   // mapping in gemm_stream_kernel); padding workgroups exit at once.
   const int nblocks = (a.N + kStN - 1) / kStN;
   const dim3 grid((unsigned)(round_up(nblocks, 8) * a.splits));
+  HCG_STAMP_ARGS(StreamArgs, a)
   // Prefetch distance by row blocks (measured, fp16, B from HBM, us, 7 / 5 /
   // 4 / 3 stages ahead): 16 x 8192 x 8192 28.2 / 27.6 / 26.7 / 25.9,
   // 32 x 8192 x 8192 29.8 / 29.2 / 28.1 / 26.8, 64 x 8192 x 8192
   // 30.1 / 29.7 / 29.5 / 29.7, 128 x 8192 x 8192 39.6 / 39.1 / 39.5 / 40.4;
   // register-staged B (16 x 8191 x 8192) 37.5 / 36.6 / 36.0 / 35.9.
   switch (a.rblocks) {
-    case 1: gemm_stream_kernel<DT, 1, UB, 3><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 2: gemm_stream_kernel<DT, 2, UB, 3><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 4: gemm_stream_kernel<DT, 4, UB, 4><<<grid, dim3(256), 0, stream>>>(a); break;
-    case 8: gemm_stream_kernel<DT, 8, UB, 5><<<grid, dim3(256), 0, stream>>>(a); break;
+    case 1: gemm_stream_kernel<DT, 1, UB, 3><<<grid, dim3(256), 0, stream>>>(HCG_STAMPED(a)); break;
+    case 2: gemm_stream_kernel<DT, 2, UB, 3><<<grid, dim3(256), 0, stream>>>(HCG_STAMPED(a)); break;
+    case 4: gemm_stream_kernel<DT, 4, UB, 4><<<grid, dim3(256), 0, stream>>>(HCG_STAMPED(a)); break;
+    case 8: gemm_stream_kernel<DT, 8, UB, 5><<<grid, dim3(256), 0, stream>>>(HCG_STAMPED(a)); break;
     default: return set_error(HCG_EINVAL, "internal: %d row blocks", a.rblocks);
   }
   HCG_HIP_CHECK(hipGetLastError());

@@ -19,7 +19,10 @@ library in the sustained state (after ``warm_s`` of back-to-back launches) and
 * per XCD: workgroups, mean shader clock (cycles over constant-clock time),
   first start and last end relative to the launch's first start;
 * ``cu_rounds``: workgroups per CU in sequence and the mean gap between
-  one's end and the next one's start on the same CU.
+  one's end and the next one's start on the same CU;
+* ``gap_after_previous_launch_us``: from the previous launch's last
+  workgroup end to this launch's first workgroup start (launches alternate
+  between two record areas), and ``launch_period_us`` between their starts.
 
 The product library never carries this code; only ``bench.py --stamps``
 loads the stamps library (in its own process).
@@ -76,7 +79,7 @@ def breakdown(records: np.ndarray) -> dict[str, Any]:
         "k_loop_cycles": _stats(rec[:, 4]),
         "start_spread_us": None,
     }
-    xcc = rec[:, 6] & 0xF
+    xcc = rec[:, 6] & 0xF  # (bits 47:8 the grid size, bit 48 the record slot)
     clock = rec[:, 5] / np.maximum(t3 - t0, 1) * REALTIME_HZ / 1e6
     per_xcd = []
     for x in sorted(set(int(v) for v in xcc)):
@@ -110,19 +113,33 @@ def breakdown(records: np.ndarray) -> dict[str, Any]:
 
 
 def run(torch: Any, cfg_name: str, *, warm_s: float = 0.3, copies: int = 1, algo: int = 0,
-        records: int = 1 << 16) -> dict[str, Any]:
+        records: int = 1 << 16, lda: int = 0, ldb: int = 0, ldc: int = 0, m: int | None = None,
+        n: int | None = None, k: int | None = None) -> dict[str, Any]:
     """Sustained launches of a workload through the stamps library; the
     breakdown of the last one.  ``copies`` > 1 rotates A and B over that many
-    copies (operands streamed from HBM rather than the Infinity Cache)."""
+    copies (operands streamed from HBM rather than the Infinity Cache);
+    ``lda``/``ldb``/``ldc`` > 0 place the operands in rows of that many
+    elements (views of wider buffers) instead of tight rows; ``m``/``n``/``k``
+    change the workload's extents (its input recipe kept)."""
     from .workloads import CONFIGS, make_inputs, to_torch
 
     cfg = CONFIGS[cfg_name]
     lib = load()
     dev = torch.device("cuda", torch.cuda.current_device())
-    a, b = make_inputs(cfg, seed=0)
-    tas = [to_torch(a, cfg.dtype, dev) for _ in range(copies)]
-    tbs = [to_torch(b, cfg.dtype, dev) for _ in range(copies)]
-    tc = torch.empty((cfg.m, cfg.n), dtype=torch.float32, device=dev)
+    a, b = make_inputs(cfg, seed=0, m=m, n=n, k=k)
+    mm, kk = a.shape
+    nn = b.shape[1]
+
+    def placed(t: Any, ld: int) -> Any:
+        if ld <= 0:
+            return t
+        buf = torch.zeros((t.shape[0], ld), dtype=t.dtype, device=dev)
+        buf[:, : t.shape[1]] = t
+        return buf[:, : t.shape[1]]
+
+    tas = [placed(to_torch(a, cfg.dtype, dev), lda) for _ in range(copies)]
+    tbs = [placed(to_torch(b, cfg.dtype, dev), ldb) for _ in range(copies)]
+    tc = placed(torch.empty((mm, nn), dtype=torch.float32, device=dev), ldc)
     buf = torch.zeros(records * WORDS, dtype=torch.int64, device=dev)
     code = 0 if cfg.dtype == "float16" else 1
     stream = torch.cuda.current_stream(dev)
@@ -130,7 +147,7 @@ def run(torch: Any, cfg_name: str, *, warm_s: float = 0.3, copies: int = 1, algo
     def launch(i: int) -> None:
         ta, tb = tas[i % copies], tbs[i % copies]
         rc = lib.hcg_gemm_algo(algo, code, ta.data_ptr(), ta.stride(0), tb.data_ptr(), tb.stride(0), tc.data_ptr(),
-                               tc.stride(0), cfg.m, cfg.n, cfg.k, stream.cuda_stream)
+                               tc.stride(0), mm, nn, kk, stream.cuda_stream)
         if rc != 0:
             raise RuntimeError(f"hcg_gemm_algo failed ({rc}): {lib.hcg_last_error().decode()}")
 
@@ -156,9 +173,25 @@ def run(torch: Any, cfg_name: str, *, warm_s: float = 0.3, copies: int = 1, algo
     finally:
         lib.hcg_stamps_set(None, 0)
     recs = buf.view(records, WORDS).cpu().numpy().view(np.uint64)
-    out = breakdown(recs)
+    # Consecutive launches alternate between two record areas (the slot bit
+    # of word 6); the later launch is the one whose workgroups end last.
+    recs = recs[recs[:, 3] != 0]
+    slot = (recs[:, 6] >> np.uint64(48)) & np.uint64(1)
+    areas = [recs[slot == s] for s in (0, 1)]
+    areas = [r for r in areas if r.size]
+    areas.sort(key=lambda r: int(r[:, 3].max()))
+    out = breakdown(areas[-1])
+    if len(areas) == 2:
+        prev, last = areas[0], areas[1]
+        us = 1e6 / REALTIME_HZ
+        p_end, l_start, p_start = int(prev[:, 3].max()), int(last[:, 0].min()), int(prev[:, 0].min())
+        out["gap_after_previous_launch_us"] = (l_start - p_end) * us
+        out["previous_launch_span_us"] = (p_end - p_start) * us
+        out["launch_period_us"] = (l_start - p_start) * us
     out["events_us"] = start.elapsed_time(end) * 1e3
     out["workload"] = cfg_name
     out["operand_copies"] = copies
-    out["k_steps_of_32"] = -(-cfg.k // 32)
+    out["ld"] = [tas[0].stride(0), tbs[0].stride(0), tc.stride(0)]
+    out["shape"] = [mm, nn, kk]
+    out["k_steps_of_32"] = -(-kk // 32)
     return out
