@@ -121,6 +121,58 @@ __global__ __launch_bounds__(256) void probe_mfma_kernel(int iters, float* sink,
   }
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (DT == 0) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                  c, 0, 0, 0);
+  }
+}
+
+// The same flops as probe_mfma_kernel per round, as 16 independent chains
+// of the 16x16x32 instruction (the streaming kernels' MFMA shape).
+template <int DT>
+__global__ __launch_bounds__(256) void probe_mfma16_kernel(int iters, float* sink, uint64_t* clocks) {
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  u32x4 fa[4], fb[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      fa[j][w] = random_pair<DT>(mix(gid * 32u + j * 4u + w));
+      fb[j][w] = random_pair<DT>(mix(gid * 32u + 16u + j * 4u + w + 0x9e3779b9u));
+    }
+  }
+  f32x4 acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = f32x4{};
+  const uint64_t t0 = __builtin_amdgcn_s_memtime();
+  const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+  for (int i = 0; i < iters; i += 4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[j] = mfma16<DT>(fa[j & 3], fb[(j + (j >> 2)) & 3], acc[j]);
+  }
+  const uint64_t t1 = __builtin_amdgcn_s_memtime();
+  const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s += acc[j][r];
+  sink[gid] = s;
+  if (threadIdx.x == 0) {
+    clocks[2 * blockIdx.x] = t1 - t0;
+    clocks[2 * blockIdx.x + 1] = r1 - r0;
+  }
+}
+
 // Strip read: workgroup w reads strip w % nstrips over run w / nstrips of
 // the rows; thread t covers 16-byte column t % width16 of rows t / width16
 // + k * (256 / width16) of each group of U row steps.
@@ -177,6 +229,21 @@ int hcg_probe_mfma(int dtype, int iters, int blocks, float* sink, uint64_t* cloc
     probe_mfma_kernel<0><<<blocks, 256, 0, s>>>(iters, sink, clocks);
   else
     probe_mfma_kernel<1><<<blocks, 256, 0, s>>>(iters, sink, clocks);
+  PROBE_HIP_CHECK(hipGetLastError());
+  t_probe_error.clear();
+  return 0;
+}
+
+int hcg_probe_mfma16(int dtype, int iters, int blocks, float* sink, uint64_t* clocks, void* stream) {
+  if (dtype != 0 && dtype != 1) return probe_error(1, "dtype must be 0 (fp16) or 1 (bf16), got %d", dtype);
+  if (iters <= 0 || blocks <= 0 || iters % 4 != 0)
+    return probe_error(1, "iters must be a positive multiple of 4 and blocks positive");
+  if (!sink || !clocks) return probe_error(1, "sink or clocks is NULL");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == 0)
+    probe_mfma16_kernel<0><<<blocks, 256, 0, s>>>(iters, sink, clocks);
+  else
+    probe_mfma16_kernel<1><<<blocks, 256, 0, s>>>(iters, sink, clocks);
   PROBE_HIP_CHECK(hipGetLastError());
   t_probe_error.clear();
   return 0;

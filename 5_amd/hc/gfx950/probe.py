@@ -20,7 +20,7 @@ from typing import Any
 from .._errors import BackendError
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libhcg_probe.so")
-EXPORTS = ("hcg_probe_mfma", "hcg_probe_read", "hcg_probe_write", "hcg_probe_last_error")
+EXPORTS = ("hcg_probe_mfma", "hcg_probe_mfma16", "hcg_probe_read", "hcg_probe_write", "hcg_probe_last_error")
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -40,6 +40,8 @@ def load() -> ctypes.CDLL:
             i64, vp, c_int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int
             lib.hcg_probe_mfma.argtypes = [c_int, c_int, c_int, vp, vp, vp]
             lib.hcg_probe_mfma.restype = c_int
+            lib.hcg_probe_mfma16.argtypes = [c_int, c_int, c_int, vp, vp, vp]
+            lib.hcg_probe_mfma16.restype = c_int
             lib.hcg_probe_read.argtypes = [vp, i64, c_int, i64, c_int, c_int, vp, vp]
             lib.hcg_probe_read.restype = c_int
             lib.hcg_probe_write.argtypes = [vp, i64, c_int, c_int, vp]
@@ -77,13 +79,15 @@ def _timed(torch: Any, stream: Any, launch: Any, warm_s: float, launches: int) -
 
 
 def mfma(torch: Any, stream: Any, dtype: int = 0, warm_s: float = 0.3, launches: int = 20,
-         iters: int = 2048, per_cu: int = 1) -> dict:
+         iters: int = 2048, per_cu: int = 1, small: bool = False) -> dict:
     """Pure MFMA issue on every CU (`per_cu` 4-wave workgroups per CU, 8
-    independent 32x32x16 chains per wave): TFLOP/s, the fraction of the
-    CUs' issue rate at the measured mean clock (the launch lasts as long as
-    the slowest XCD's clock allows, so this stays below 1), shader cycles
-    per MFMA inside the loop (32 at the full issue rate), and the shader
-    clock (cycles over 100 MHz real-time ticks, per workgroup)."""
+    independent 32x32x16 chains per wave, or with `small` 16 chains of
+    16x16x32, the same flops): TFLOP/s, the fraction of the CUs' issue rate
+    at the measured mean clock (the launch lasts as long as the slowest
+    XCD's clock allows, so this stays below 1), shader cycles per MFMA
+    inside the loop (32 for 32x32x16 and 16 for 16x16x32 at the full issue
+    rate), and the shader clock (cycles over 100 MHz real-time ticks, per
+    workgroup)."""
     lib = load()
     dev = torch.cuda.current_device()
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
@@ -91,9 +95,11 @@ def mfma(torch: Any, stream: Any, dtype: int = 0, warm_s: float = 0.3, launches:
     sink = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
     clocks = torch.zeros(2 * blocks, dtype=torch.int64, device="cuda")
 
+    entry = lib.hcg_probe_mfma16 if small else lib.hcg_probe_mfma
+
     def launch() -> None:
-        _check(lib, lib.hcg_probe_mfma(dtype, iters, blocks, sink.data_ptr(), clocks.data_ptr(),
-                                       stream.cuda_stream), "hcg_probe_mfma")
+        _check(lib, entry(dtype, iters, blocks, sink.data_ptr(), clocks.data_ptr(), stream.cuda_stream),
+               "hcg_probe_mfma16" if small else "hcg_probe_mfma")
 
     seconds = _timed(torch, stream, launch, warm_s, launches)
     flops = blocks * 4 * 8 * iters * 2 * 32 * 32 * 16
@@ -103,11 +109,13 @@ def mfma(torch: Any, stream: Any, dtype: int = 0, warm_s: float = 0.3, launches:
     # 4096 fp16/bf16 flop per clock per CU (four SIMDs, one 32x32x16 MFMA
     # per 32 clocks each)
     issue = tflops * 1e12 / (cus * 4096 * float(mhz.mean()) * 1e6)
+    chains = 16 if small else 8
     return {"dtype": "f16" if dtype == 0 else "bf16", "tflops": tflops, "issue_frac": issue,
-            "cycles_per_mfma": float(c[:, 0].mean()) / (iters * 8),
+            "cycles_per_mfma": float(c[:, 0].mean()) / (iters * chains),
             "us_per_launch": seconds * 1e6, "clock_mhz": float(mhz.mean()),
             "clock_mhz_min": float(mhz.min()), "clock_mhz_max": float(mhz.max()),
-            "shape": f"{blocks} workgroups x 4 waves x 8 chains x {iters} rounds of v_mfma_f32_32x32x16"}
+            "shape": f"{blocks} workgroups x 4 waves x {chains} chains x {iters} rounds of "
+                     f"v_mfma_f32_{'16x16x32' if small else '32x32x16'}"}
 
 
 MALL_BYTES = 256 << 20  # MI355X Infinity Cache
@@ -156,13 +164,14 @@ def write(torch: Any, stream: Any, nbytes: int, blocks: int, nontemporal: bool, 
 
 def ceilings(torch: Any, stream: Any) -> dict:
     """What this board sustains, measured now: pure MFMA issue (fp16 and
-    bf16, random operands), streaming HBM read (1 GiB, contiguous and in
+    bf16, random operands; and fp16 as 16x16x32), streaming HBM read (1 GiB, contiguous and in
     1 KB strips of 16 KB rows; and at the skinny GEMM's size, 128 MiB of
     16 KB rows in 256-byte strips, the pattern its kernel streams B in) and
     streaming HBM write (1 GiB).  Each read figure is the best of a few
     launch shapes; every launch reads HBM (rotating copies)."""
     gib, mib = 1 << 30, 1 << 20
-    out: dict = {"mfma_f16": mfma(torch, stream, 0), "mfma_bf16": mfma(torch, stream, 1)}
+    out: dict = {"mfma_f16": mfma(torch, stream, 0), "mfma_bf16": mfma(torch, stream, 1),
+                 "mfma16_f16": mfma(torch, stream, 0, small=True)}
     reads = [read(torch, stream, 4096, 4096, gib, 2048, 8), read(torch, stream, 16384, 1024, gib, 16, 8)]
     out["hbm_read"] = max(reads, key=lambda r: r["gbs"])
     c4 = [read(torch, stream, 16384, 256, 128 * mib, 4, 4), read(torch, stream, 4096, 4096, 128 * mib, 256, 8)]

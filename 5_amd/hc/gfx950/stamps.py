@@ -114,13 +114,14 @@ def breakdown(records: np.ndarray) -> dict[str, Any]:
 
 def run(torch: Any, cfg_name: str, *, warm_s: float = 0.3, copies: int = 1, algo: int = 0,
         records: int = 1 << 16, lda: int = 0, ldb: int = 0, ldc: int = 0, m: int | None = None,
-        n: int | None = None, k: int | None = None) -> dict[str, Any]:
+        n: int | None = None, k: int | None = None, raw: bool = False) -> dict[str, Any]:
     """Sustained launches of a workload through the stamps library; the
     breakdown of the last one.  ``copies`` > 1 rotates A and B over that many
     copies (operands streamed from HBM rather than the Infinity Cache);
     ``lda``/``ldb``/``ldc`` > 0 place the operands in rows of that many
     elements (views of wider buffers) instead of tight rows; ``m``/``n``/``k``
-    change the workload's extents (its input recipe kept)."""
+    change the workload's extents (its input recipe kept); ``raw`` adds the
+    last launch's records as ``records`` (workgroup index -> 8 words)."""
     from .workloads import CONFIGS, make_inputs, to_torch
 
     cfg = CONFIGS[cfg_name]
@@ -175,11 +176,16 @@ def run(torch: Any, cfg_name: str, *, warm_s: float = 0.3, copies: int = 1, algo
     recs = buf.view(records, WORDS).cpu().numpy().view(np.uint64)
     # Consecutive launches alternate between two record areas (the slot bit
     # of word 6); the later launch is the one whose workgroups end last.
-    recs = recs[recs[:, 3] != 0]
+    index = np.nonzero(recs[:, 3])[0]
+    recs = recs[index]
     slot = (recs[:, 6] >> np.uint64(48)) & np.uint64(1)
-    areas = [recs[slot == s] for s in (0, 1)]
-    areas = [r for r in areas if r.size]
-    areas.sort(key=lambda r: int(r[:, 3].max()))
+    grid = (recs[:, 6] >> np.uint64(8)) & np.uint64((1 << 40) - 1)
+    wg = (index - slot * grid).astype(np.int64)  # record b of slot s sits at s * grid + b
+    areas = [(recs[slot == s], wg[slot == s]) for s in (0, 1)]
+    areas = [a for a in areas if a[0].size]
+    areas.sort(key=lambda a: int(a[0][:, 3].max()))
+    last_wg = areas[-1][1]
+    areas = [a[0] for a in areas]
     out = breakdown(areas[-1])
     if len(areas) == 2:
         prev, last = areas[0], areas[1]
@@ -189,6 +195,8 @@ def run(torch: Any, cfg_name: str, *, warm_s: float = 0.3, copies: int = 1, algo
         out["previous_launch_span_us"] = (p_end - p_start) * us
         out["launch_period_us"] = (l_start - p_start) * us
     out["events_us"] = start.elapsed_time(end) * 1e3
+    if raw:
+        out["records"] = {int(b): [int(x) for x in r] for b, r in zip(last_wg, areas[-1])}
     out["workload"] = cfg_name
     out["operand_copies"] = copies
     out["ld"] = [tas[0].stride(0), tbs[0].stride(0), tc.stride(0)]

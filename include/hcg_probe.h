@@ -7,6 +7,7 @@
  *
  *   hcg_probe_mfma   -- pure MFMA issue (v_mfma_f32_32x32x16_{f16,bf16})
  *                       on every CU, with the shader clock it ran at;
+ *   hcg_probe_mfma16 -- the same flops as v_mfma_f32_16x16x32_{f16,bf16};
  *   hcg_probe_read   -- streaming HBM read of a 2-D region in strips
  *                       (the access pattern of the streaming GEMM kernels)
  *                       or contiguously;
@@ -33,6 +34,10 @@ extern "C" {
  * cycles (s_memtime) and the 100 MHz real-time ticks (s_memrealtime) its
  * first wave spent in the loop. */
 int hcg_probe_mfma(int dtype, int iters, int blocks, float* sink, uint64_t* clocks, void* stream);
+
+/* As hcg_probe_mfma with 16 independent 16x16x32 MFMAs per round (the same
+ * 2 * 16 * 16 * 32 * 16 * iters flops per wave as 8 of 32x32x16). */
+int hcg_probe_mfma16(int dtype, int iters, int blocks, float* sink, uint64_t* clocks, void* stream);
 
 /* Reads `rows` rows of `pitch` bytes from `src`: the row is cut into
  * strips of `width` bytes (16 <= width <= 4096, a power of two dividing

@@ -46,6 +46,8 @@ def test_probe_library_exports_what_its_header_declares():
     # bad arguments are rejected on the host, before any launch
     assert lib.hcg_probe_mfma(2, 1, 1, 0x1000, 0x1000, None) == 1
     assert "dtype" in lib.hcg_probe_last_error().decode()
+    assert lib.hcg_probe_mfma16(0, 6, 1, 0x1000, 0x1000, None) == 1
+    assert "multiple of 4" in lib.hcg_probe_last_error().decode()
     assert lib.hcg_probe_read(0x1000, 4096, 24, 8, 1, 4, 0x1000, None) == 1
     assert "power of two" in lib.hcg_probe_last_error().decode()
     assert lib.hcg_probe_read(0x1000, 4096, 256, 8, 1, 3, 0x1000, None) == 1
