@@ -44,9 +44,10 @@ when the kernel *is* that GEMM, so a kernel is accepted only after two checks:
    kernel replaces the whole loop of them.  The inputs are integers, so every
    summation order is exact and C must equal A @ B exactly; an element left
    unwritten (C starts as NaN) or any other value rejects the kernel.  Two
-   runs are made: one with small values, and one whose partial sums reach
-   ~10^6, which only float32 accumulation computes exactly (the reference
-   folds in np.float32, examples/amdgpu_gfx11_wmma_matmul.py:183-190); the
+   runs are made: one with small values, and one (one workgroup's tile, K
+   one and a half steps plus one) whose partial sums reach ~10^6, which
+   only float32 accumulation computes exactly (the reference folds in
+   np.float32, examples/amdgpu_gfx11_wmma_matmul.py:183-190); the
    accumulator the init and accumulate helpers return must be float32.
 
 A kernel that fails either check raises ``LaunchError`` naming it and the
@@ -740,7 +741,10 @@ _PROBES = ("small", "wide")
 
 
 def _probe_inputs(tm: int, tn: int, tk: int, dtype: str, probe: str) -> tuple[np.ndarray, np.ndarray]:
-    m, n, k = tm + tm // 2 + 1, tn + tn // 2 + 1, tk + tk // 2 + 1
+    # The small probe masks every tail (each extent one and a half tiles plus
+    # one); the wide one tests the accumulation only: one workgroup's tile,
+    # over a K of one and a half K steps plus one.
+    m, n, k = (tm + tm // 2 + 1, tn + tn // 2 + 1, tk + tk // 2 + 1) if probe == "small" else (tm, tn, tk + tk // 2 + 1)
     rng = np.random.default_rng(0x5EED if probe == "small" else 0x5EED + 1)
     # bfloat16 kernels see their values as float32 payloads.
     payload = np.float16 if dtype == "float16" else np.float32
