@@ -54,6 +54,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 #include <type_traits>
@@ -380,11 +381,11 @@ __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f
 #ifdef HCG_STAMPS
 __device__ uint64_t* g_stamp_buf = nullptr;
 __device__ int64_t g_stamp_cap = 0;
-int g_stamp_launches = 0;  // host: launches so far (their parity is the slot)
+std::atomic<int> g_stamp_launches{0};  // host: launches so far (their parity is the slot)
 #define HCG_STAMP_SLOT(g) (g).stamp_slot
 #define HCG_STAMP_ARGS(Args, a) \
   Args a##_s = a;               \
-  a##_s.stamp_slot = g_stamp_launches++ & 1;
+  a##_s.stamp_slot = g_stamp_launches.fetch_add(1, std::memory_order_relaxed) & 1;
 #define HCG_STAMPED(a) a##_s
 #else
 #define HCG_STAMP_SLOT(g) 0
