@@ -597,7 +597,7 @@ def main() -> int:
         "board": board_state(torch, stream, step, 2.5),
     }
     del ta, tb, tc
-    if not args.no_extra and not is_skinny:
+    if not args.no_extra and not is_skinny and cfg.flops >= 1e9:  # (a launch-bound 128^3 GEMM has no cold case)
         log(f"bench: {cfg.name} cold (operands rotated)")
         cold = bench_cold(torch, g, stream, cfg.name, args.steps, args.warmup)
         cold["note"] = "value uses the warm figure; this one reads A and B from HBM on every launch"
