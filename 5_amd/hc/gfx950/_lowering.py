@@ -170,7 +170,7 @@ def check_matrix_op(op: RecordedOp, target: str, intrinsic: Any, args: tuple[Any
     if op.results != (want_type,):
         raise LoweringError(f"intrinsic {name!r}: its {op.name} op's results are {list(op.results)}, "
                             f"not one {want_type}")
-    positional = [a for a in args]
+    positional = list(args)
     if len(op.operands) != 3 or not all(any(o is a for a in positional) for o in op.operands):
         raise LoweringError(f"intrinsic {name!r}: its {op.name} op must take three of the call's arguments "
                             "(A, B, accumulator)")
