@@ -112,6 +112,23 @@ def breakdown(records: np.ndarray) -> dict[str, Any]:
     return out
 
 
+def split_launches(buffer: np.ndarray) -> list[tuple[np.ndarray, np.ndarray]]:
+    """The (records, workgroup indices) of the launches in a stamps buffer,
+    earlier launch first.  Consecutive launches alternate between two record
+    areas: record b of slot s sits at s * grid + b, and word 6 carries the
+    slot (bit 48) and the grid size (bits 47:8); unwritten records are zero.
+    The later launch is the one whose workgroups end last."""
+    index = np.nonzero(buffer[:, 3])[0]
+    recs = buffer[index]
+    slot = (recs[:, 6] >> np.uint64(48)) & np.uint64(1)
+    grid = (recs[:, 6] >> np.uint64(8)) & np.uint64((1 << 40) - 1)
+    wg = index.astype(np.int64) - (slot * grid).astype(np.int64)
+    areas = [(recs[slot == s], wg[slot == s]) for s in (0, 1)]
+    areas = [a for a in areas if a[0].size]
+    areas.sort(key=lambda a: int(a[0][:, 3].max()))
+    return areas
+
+
 def run(torch: Any, cfg_name: str, *, warm_s: float = 0.3, copies: int = 1, algo: int = 0,
         records: int = 1 << 16, lda: int = 0, ldb: int = 0, ldc: int = 0, m: int | None = None,
         n: int | None = None, k: int | None = None, raw: bool = False) -> dict[str, Any]:
@@ -174,21 +191,11 @@ def run(torch: Any, cfg_name: str, *, warm_s: float = 0.3, copies: int = 1, algo
     finally:
         lib.hcg_stamps_set(None, 0)
     recs = buf.view(records, WORDS).cpu().numpy().view(np.uint64)
-    # Consecutive launches alternate between two record areas (the slot bit
-    # of word 6); the later launch is the one whose workgroups end last.
-    index = np.nonzero(recs[:, 3])[0]
-    recs = recs[index]
-    slot = (recs[:, 6] >> np.uint64(48)) & np.uint64(1)
-    grid = (recs[:, 6] >> np.uint64(8)) & np.uint64((1 << 40) - 1)
-    wg = (index - slot * grid).astype(np.int64)  # record b of slot s sits at s * grid + b
-    areas = [(recs[slot == s], wg[slot == s]) for s in (0, 1)]
-    areas = [a for a in areas if a[0].size]
-    areas.sort(key=lambda a: int(a[0][:, 3].max()))
-    last_wg = areas[-1][1]
-    areas = [a[0] for a in areas]
-    out = breakdown(areas[-1])
-    if len(areas) == 2:
-        prev, last = areas[0], areas[1]
+    launches = split_launches(recs)
+    last, last_wg = launches[-1]
+    out = breakdown(last)
+    if len(launches) == 2:
+        prev = launches[0][0]
         us = 1e6 / REALTIME_HZ
         p_end, l_start, p_start = int(prev[:, 3].max()), int(last[:, 0].min()), int(prev[:, 0].min())
         out["gap_after_previous_launch_us"] = (l_start - p_end) * us
@@ -196,7 +203,7 @@ def run(torch: Any, cfg_name: str, *, warm_s: float = 0.3, copies: int = 1, algo
         out["launch_period_us"] = (l_start - p_start) * us
     out["events_us"] = start.elapsed_time(end) * 1e3
     if raw:
-        out["records"] = {int(b): [int(x) for x in r] for b, r in zip(last_wg, areas[-1])}
+        out["records"] = {int(b): [int(x) for x in r] for b, r in zip(last_wg, last)}
     out["workload"] = cfg_name
     out["operand_copies"] = copies
     out["ld"] = [tas[0].stride(0), tbs[0].stride(0), tc.stride(0)]

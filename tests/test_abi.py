@@ -200,3 +200,25 @@ def test_stamps_library_is_built_apart_and_its_records_reduce():
     assert out["per_xcd"][0]["xcd"] == 3 and abs(out["per_xcd"][0]["clock_mhz"] - 2000) < 1e-9
     assert out["cu_rounds"] == {"cus": 2, "max_per_cu": 2, "min_per_cu": 1, "mean_gap_us": 1.0}
     assert out["start_spread_us"] == 0.1
+
+
+def test_stamps_buffer_splits_into_two_consecutive_launches():
+    """Records of two launches of a 3-workgroup grid: slot 1 (the earlier
+    launch here) at records 3..5, slot 0 (later) at 0..2; workgroup 1 of the
+    later launch never wrote (a padding workgroup)."""
+    import numpy as np
+
+    from hc.gfx950 import stamps
+
+    def rec(t0, t3, slot, grid=3):
+        return [t0, t0 + 10, t3 - 10, t3, 0, 0, 5 | (grid << 8) | (slot << 48), 0]
+
+    buf = np.zeros((8, 8), dtype=np.uint64)
+    buf[0] = rec(2000, 2900, 0)
+    buf[2] = rec(2010, 2950, 0)
+    buf[3] = rec(1000, 1800, 1)
+    buf[4] = rec(1005, 1850, 1)
+    buf[5] = rec(1010, 1900, 1)
+    (prev, prev_wg), (last, last_wg) = stamps.split_launches(buf)
+    assert list(prev_wg) == [0, 1, 2] and list(last_wg) == [0, 2]
+    assert int(prev[:, 3].max()) == 1900 and int(last[:, 0].min()) == 2000
