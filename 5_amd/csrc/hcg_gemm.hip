@@ -371,13 +371,14 @@ __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f
 // clock (s_memtime) at the workgroup's start (0), the end of its prologue
 // (1), the end of its K loop (2); write() waits for the workgroup's stores
 // to be acknowledged, marks its end (3) and has lane 0 store, with vector
-// stores, one record of 8 words at g_stamp_buf + 8 * blockIdx.x:
+// stores, one record of 8 words at g_stamp_buf + 8 * (slot * gridDim.x +
+// blockIdx.x):
 //   [0..3] clock at marks 0..3, [4] shader cycles of the K loop (2 - 1),
 //   [5] shader cycles start to end (3 - 0), [6] XCC id (bits 3:0), grid size
 //   (bits 47:8) and record slot (bit 48), [7] HW_ID.
 // hcg_stamps_set() names the buffer; bench.py --stamps reads it.  Launches
-// alternate between two record areas (slot 0 at record blockIdx.x, slot 1 at
-// gridDim.x + blockIdx.x), so two consecutive launches can be compared.
+// alternate between the two slots (record areas), so two consecutive
+// launches can be compared.
 #ifdef HCG_STAMPS
 __device__ uint64_t* g_stamp_buf = nullptr;
 __device__ int64_t g_stamp_cap = 0;
