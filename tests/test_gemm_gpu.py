@@ -1214,3 +1214,33 @@ def test_compiled_binding_matches_the_ctypes_path(m, n, k, dtype):
     g.gemm(ta, tbt, out=out)
     torch.cuda.synchronize()
     assert torch.equal(out, via_ctypes)
+
+
+# Edge tiles whose C rows are 16-byte aligned (ldc a multiple of 4, N a
+# multiple of 4) store whole chunks non-temporally and skip rows past M and
+# chunks past N; C here is a view into a NaN-filled buffer with extra columns
+# and rows, so a chunk stored past N or a row past M would show.
+_ALIGNED_C_CASES = [
+    ("auto", 300, 520, 200), ("auto", 4095, 3008, 96), ("auto", 1000, 1000, 300), ("tiled_256x256", 257, 260, 64),
+    ("tiled_256x192", 255, 196, 40), ("tiled_128x256", 129, 260, 33), ("tiled_128x128", 130, 132, 70),
+    ("tiled_256x64", 300, 68, 50), ("tiled", 520, 4, 2000), ("auto", 17, 1028, 257),
+]
+
+
+@pytest.mark.parametrize("algo,m,n,k", _ALIGNED_C_CASES)
+def test_aligned_c_rows_edge_tiles_write_only_inside(algo, m, n, k):
+    import hc.gfx950 as g
+    from hc.gfx950.workloads import make_inputs
+
+    assert n % 4 == 0
+    print(f"case aligned C {algo} {m}x{n}x{k}", flush=True)
+    a, b = make_inputs("c2_4096_f16", seed=m + n + k, m=m, n=n, k=k)
+    ldc = n + 8  # 16-byte aligned rows with 8 guard columns
+    guard = torch.full((m + 3, ldc), float("nan"), dtype=torch.float32, device=DEV)
+    g.gemm(_dev(a), _dev(b), out=guard[:m, :n], algo=algo)
+    torch.cuda.synchronize()
+    host = guard.cpu().numpy()
+    _check(host[:m, :n], oracle.gemm_c(a, b), k)
+    mask = np.ones_like(host, dtype=bool)
+    mask[:m, :n] = False
+    assert np.all(np.isnan(host[mask]))
