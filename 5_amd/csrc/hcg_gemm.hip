@@ -2123,10 +2123,18 @@ __global__ __launch_bounds__(64 * kSrWaves) void split_reduce_kernel(const float
   }
 }
 
+// Grid-stride: a launch holds at most 2^32 - 1 work-items, and C may hold
+// more elements than that.
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* C, int64_t ldc, int M, int N) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)M * N) return;
-  C[(idx / N) * ldc + (idx % N)] = 0.0f;
+  const int64_t total = (int64_t)M * N, stride = (int64_t)gridDim.x * 256;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += stride)
+    C[(idx / N) * ldc + (idx % N)] = 0.0f;
+}
+
+constexpr int64_t kFillMaxBlocks = (int64_t)1 << 20;
+unsigned fill_blocks(int64_t total) {
+  const int64_t blocks = (total + 255) / 256;
+  return (unsigned)(blocks < kFillMaxBlocks ? blocks : kFillMaxBlocks);
 }
 
 
@@ -3102,7 +3110,7 @@ int gemm_impl(int algo, int dtype, const void* A, int64_t lda, const void* B, in
 
   if (K == 0) {
     const int64_t total = M * N;
-    fill_zero_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(C, ldc, (int)M, (int)N);
+    fill_zero_kernel<<<fill_blocks(total), 256, 0, stream>>>(C, ldc, (int)M, (int)N);
     HCG_HIP_CHECK(hipGetLastError());
     t_last_error.clear();
     return HCG_OK;

@@ -838,6 +838,43 @@ def test_k_zero_writes_zeros_and_empty_output_is_untouched():
     g.gemm(torch.zeros((0, 5), dtype=torch.float16, device=DEV), torch.zeros((5, 30), dtype=torch.float16, device=DEV), out=e)
 
 
+def test_k_zero_output_over_2_to_32_elements():
+    """K = 0 writes zeros over a C of more than 2^32 elements (a launch holds
+    fewer work-items than that), a view in a NaN buffer whose other columns
+    and row stay untouched."""
+    import hc.gfx950 as g
+
+    m, n, ld = 65537, 65536, 65540
+    print(f"case K=0 C of {m * n} elements", flush=True)
+    buf = torch.full((m + 1, ld), float("nan"), dtype=torch.float32, device=DEV)
+    a = torch.zeros((m, 0), dtype=torch.float16, device=DEV)
+    b = torch.zeros((0, n), dtype=torch.float16, device=DEV)
+    g.gemm(a, b, out=buf[:m, :n])
+    torch.cuda.synchronize()
+    assert bool((buf[:m, :n] == 0).all())
+    assert bool(torch.isnan(buf[:m, n:]).all()) and bool(torch.isnan(buf[m:]).all())
+    del buf
+
+
+# C over 2 GiB on each kernel family that writes C directly (the tiled
+# kernel, the streaming kernel, the narrow kernel): small-integer inputs make
+# every sum exact, so float32 products on the host are the exact answer.
+@pytest.mark.parametrize("algo,m,n,k", [("auto", 24000, 24000, 40), ("skinny", 128, 4200000, 40),
+                                        ("narrow", 8400000, 64, 40)])
+def test_output_over_2gib_bit_exact(algo, m, n, k):
+    import hc.gfx950 as g
+
+    print(f"case C over 2 GiB {algo} m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(m + n)
+    ai = rng.integers(-3, 4, size=(m, k)).astype(np.float32)
+    bi = rng.integers(-3, 4, size=(k, n)).astype(np.float32)
+    c = g.gemm(torch.from_numpy(ai).to(DEV).half(), torch.from_numpy(bi).to(DEV).half(), algo=algo)
+    torch.cuda.synchronize()
+    got = c.cpu().numpy()
+    del c
+    assert np.array_equal(got, ai @ bi)  # |sums| <= 360: exact in float32
+
+
 def test_two_streams_use_separate_workspaces():
     """The split-K workspace is per stream: two streams running skinny GEMMs
     concurrently must not corrupt each other."""
