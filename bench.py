@@ -27,9 +27,10 @@ metric configuration, fp16 M=N=K=4096; ``value`` is TFLOP/s
   sampled from the driver while the headline workload runs;
 * ``ceiling``: what this board sustains, measured in the same run by the
   probes of libhcg_probe.so (include/hcg_probe.h): pure MFMA issue (TFLOP/s
-  and shader clock), streaming HBM read and write (GB/s); ``roofline`` and
-  ``skinny`` carry ``frac_of_ceiling`` beside ``frac`` (which stays against
-  the 2516.6 TFLOP/s and 8 TB/s nameplate peaks).
+  and shader clock), streaming HBM read and write (GB/s); ``roofline``,
+  ``skinny`` and each of ``others`` (warm and cold; against the MFMA ceiling
+  of its input type) carry ``frac_of_ceiling`` beside ``frac`` (which stays
+  against the 2516.6 TFLOP/s and 8 TB/s nameplate peaks).
 
 ``--ceilings-only`` runs just the probes (for rocprofv3).  ``--stamps
 WORKLOAD`` runs a workload through the timestamped build of the library and
@@ -629,6 +630,14 @@ def main() -> int:
             sk = result["skinny"]
             sk["frac_of_ceiling"] = sk["value"] / ceiling["hbm_read_128mib"]["gbs"]
             sk["ceiling_source"] = "ceiling.hbm_read_128mib"
+        # The other compute-bound workloads against the same board's MFMA
+        # ceiling of their input type.
+        for name, other in result.get("others", {}).items():
+            mkey = "mfma_bf16" if CONFIGS[name].dtype == "bfloat16" else "mfma_f16"
+            for entry in (other, other.get("cold")):
+                if entry:
+                    entry["frac_of_ceiling"] = entry["value"] / ceiling[mkey]["tflops"]
+                    entry["ceiling_source"] = f"ceiling.{mkey}"
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (oracle)")
         result["cpu_baseline"] = cpu_baseline(cfg, a, b, args.cpu_seconds)
